@@ -1,0 +1,247 @@
+#!/usr/bin/env python
+"""Headline benchmark: geomean of the median ms over configs 2-5 on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,3,4,5]
+
+One step is one call of the drop-in forward pass ``fn(A) -> (H, tau)`` on one
+config's full batch, with A already resident in HBM. For each config: the FP64
+gates are checked once on the actual input, W untimed warm-up steps run, then
+exactly K steps are timed, each with its own HIP event pair on the current
+stream and a device synchronise (the reference's convention,
+src/qrbench/bench.py:57-77); the whole K-step region is also bracketed by
+synchronises and timed. ``value`` is the geomean over configs of the per-config
+median ms. One JSON line is printed last.
+
+Also reported:
+- per config: median ms, GFLOP/s (4/3 n^3 batch), fraction of the MI355X FP32
+  matrix peak, and algorithmic HBM GB/s ((2n^2+n)*4 B per matrix);
+- roofline: the kernel with the largest traced time over the configs, its
+  algorithmic flops (or bytes) per launch over its mean HIP-event duration,
+  recorded on the stream the kernel is launched on (library launch tracer);
+- cpu_baseline: torch.geqrf on the host's CPU cores, on a bounded sample of
+  each config's batch (same inputs), scaled to the full batch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "geomean median ms (cfg 2-5); GFLOP/s (4/3·n³·b) & % MI355X FP32 peak"
+
+# Matrices per config factored by the CPU baseline (bounded sample).
+CPU_SAMPLE = {1: 64, 2: 256, 3: 16, 4: 4, 5: 1}
+
+
+def _ms_events(fn, A, torch):
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    fn(A)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e)
+
+
+def run_config(cfg: int, steps: int, warmup: int, torch, trace_kernels) -> dict:
+    from gpumode_qr_amd import _lib, bench, checker, hip_qr, inputs
+
+    prob = inputs.make_config_problem(cfg, device="cuda")
+    A = prob.tensor
+    b, n = prob.batch, prob.n
+    ws = torch.empty(max(1, hip_qr.workspace_bytes(b, n)), dtype=torch.uint8, device="cuda")
+
+    def fn(x):
+        return hip_qr.geqrf(x, workspace=ws)
+
+    H, tau = fn(A)
+    torch.cuda.synchronize()
+    chk = checker.check(A, H, tau)
+    del H, tau
+    torch.cuda.synchronize()
+    print(f"[bench] {prob.name}: gates {'PASS' if chk.passed else 'FAIL'} "
+          f"factor={chk.factor_residual:.2e}/{chk.factor_threshold:.2e} "
+          f"orth={chk.orth_residual:.2e}/{chk.orth_threshold:.2e}", flush=True)
+
+    for _ in range(warmup):
+        fn(A)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    times = [_ms_events(fn, A, torch) for _ in range(steps)]
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    med = statistics.median(times)
+    flops = bench.qr_flops(b, n)
+    algo_bytes = bench.qr_bytes(b, n)
+
+    # Per-kernel event timing, in a separate pass so the events do not perturb
+    # the timed steps above.
+    _lib.trace_reset()
+    _lib.trace_enable(trace_kernels)
+    for _ in range(max(1, min(steps, 5))):
+        fn(A)
+    torch.cuda.synchronize()
+    _lib.trace_enable(None)
+    kernels = {k: _lib.trace_read(k) for k in trace_kernels}
+    _lib.trace_reset()
+
+    row = {
+        "cfg": cfg,
+        "name": prob.name,
+        "batch": b,
+        "n": n,
+        "median_ms": med,
+        "min_ms": min(times),
+        "wall_ms_per_step": wall_ms / steps,
+        "gflops": flops / (med * 1e-3) / 1e9,
+        "pct_fp32_peak": 100.0 * flops / (med * 1e-3) / (FP32_MFMA_PEAK_TFLOPS * 1e12),
+        "hbm_gbs": algo_bytes / (med * 1e-3) / 1e9,
+        "gates_pass": chk.passed,
+        "factor_residual": chk.factor_residual,
+        "orth_residual": chk.orth_residual,
+        "kernels": kernels,
+    }
+    print(f"[bench] {prob.name}: median {med:.4f} ms  {row['gflops']:.0f} GFLOP/s "
+          f"({row['pct_fp32_peak']:.2f}% fp32 peak)  {row['hbm_gbs']:.0f} GB/s algorithmic",
+          flush=True)
+    del A, ws
+    torch.cuda.empty_cache()
+    return row
+
+
+def cpu_baseline(cfgs: list[int], torch) -> dict:
+    """torch.geqrf on the CPU for a bounded sample of each config (same inputs)."""
+    from gpumode_qr_amd import bench, inputs
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    per_cfg = {}
+    for cfg in cfgs:
+        spec = inputs.CONFIGS[cfg - 1]
+        A = inputs.config_tensor(spec)
+        k = min(CPU_SAMPLE.get(cfg, 1), A.shape[0])
+        sample = A[:k].contiguous()
+        torch.geqrf(sample)  # warm-up
+        reps = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            torch.geqrf(sample)
+            reps.append(time.perf_counter() - t0)
+        t = statistics.median(reps)
+        full_ms = t * 1e3 * A.shape[0] / k
+        per_cfg[cfg] = {"sample_matrices": k, "sample_ms": t * 1e3, "full_batch_ms_est": full_ms,
+                        "gflops": bench.qr_flops(A.shape[0], A.shape[1]) / (full_ms * 1e-3) / 1e9}
+        print(f"[cpu] cfg{cfg}: torch.geqrf {k} of {A.shape[0]} matrices in {t * 1e3:.1f} ms "
+              f"-> {full_ms:.1f} ms full batch ({cores} threads)", flush=True)
+    gm = bench.geomean([v["full_batch_ms_est"] for v in per_cfg.values()])
+    return {
+        "value": gm,
+        "unit": "ms (geomean of per-config full-batch estimates)",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": "torch.geqrf (LAPACK sgeqrf, the reference's torch_geqrf baseline) on the CPU, "
+                  + ", ".join(f"cfg{c}: {v['sample_matrices']} matrices"
+                              for c, v in per_cfg.items())
+                  + "; median of 3, scaled linearly to the full batch",
+        "per_config": per_cfg,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--configs", default="2,3,4,5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the batch would shard across GPUs with no exchange). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    from gpumode_qr_amd import _lib, bench
+
+    _lib.load()
+    cfgs = [int(c) for c in args.configs.split(",") if c.strip()]
+    trace_kernels = ["smalln", "panel", "wy_w2", "wy_apply", "copy"]
+    rows = [run_config(c, args.steps, args.warmup, torch, trace_kernels) for c in cfgs]
+    gm = bench.geomean([r["median_ms"] for r in rows])
+
+    # Dominant kernel: largest traced time summed over the configs.
+    totals = {}
+    for k in trace_kernels:
+        ms = sum(r["kernels"][k]["ms"] for r in rows)
+        if ms > 0:
+            totals[k] = ms
+    dom = max(totals, key=totals.get)
+    launches = sum(r["kernels"][dom]["launches"] for r in rows)
+    dom_ms = sum(r["kernels"][dom]["ms"] for r in rows)
+    dom_flops = sum(r["kernels"][dom]["flops"] for r in rows)
+    dom_bytes = sum(r["kernels"][dom]["bytes"] for r in rows)
+    if dom in ("smalln", "copy"):
+        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    else:
+        achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s"}
+    roof.update({
+        "frac": roof["achieved"] / roof["peak"],
+        "traffic": None,
+        "kernel": dom,
+        "launches": launches,
+        "mean_launch_us": dom_ms * 1e3 / max(launches, 1),
+        "share_of_traced_time": dom_ms / sum(totals.values()),
+    })
+
+    cpu = None if args.no_cpu else cpu_baseline(cfgs, torch)
+    out = {
+        "metric": METRIC,
+        "value": gm,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": gm,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded CPU generators (gpumode_qr_amd.inputs.CONFIGS), copied to HBM",
+        "config": {
+            "workload": "batched compact-Householder QR fp32 (torch.geqrf layout), configs "
+                        + ",".join(str(c) for c in cfgs),
+            "per_config": [
+                {k: r[k] for k in ("cfg", "name", "batch", "n", "median_ms", "min_ms", "gflops",
+                                   "pct_fp32_peak", "hbm_gbs", "gates_pass")}
+                for r in rows
+            ],
+            "all_gates_pass": all(r["gates_pass"] for r in rows),
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0 if out["config"]["all_gates_pass"] else 3
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

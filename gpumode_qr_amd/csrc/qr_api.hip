@@ -1,0 +1,321 @@
+// qr_api.hip -- the C ABI of libqr_gfx950.so (include/qr_gfx950.h), the
+// blocked factorisation driver, and per-launch event tracing.
+//
+// Driver (reference: _hh_panel_blocked_qr, src/qrbench/variants.py:761-805, and
+// the n <= 128 fused route of make_hh_fused_smalln, :739-758):
+//   n <= 64 : one launch of the fused small-n kernel (A -> H directly).
+//   n >  64 : copy A -> H, then for each 16-wide panel at column j0:
+//             panel kernel (V and tau in place, T to the workspace), then the
+//             trailing update C -= V T^T V^T C on the columns to its right
+//             (W2 = T^T V^T C kernel, then the C -= V W2 kernel).
+// Everything is enqueued on the caller's stream; nothing synchronises except
+// qr_trace_read, which waits for the events it reads.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/qr_gfx950.h"
+
+namespace qr {
+hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                               int64_t sHb, float* tau, int64_t sTb, int batch, int n,
+                               hipStream_t stream);
+hipError_t launch_panel16(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
+                          int64_t sTaub, float* T, int64_t sTb, int batch, hipStream_t stream);
+hipError_t launch_wy_w2_16(const float* H, int64_t sHb, int64_t ldh, int j0, int r, int c,
+                           const float* T, int64_t sTb, float* W2, int64_t sWb, int batch,
+                           hipStream_t stream);
+hipError_t launch_wy_apply_16(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c,
+                              const float* W2, int64_t sWb, int batch, hipStream_t stream);
+hipError_t launch_copy_in(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                          int64_t sHb, int batch, int n, hipStream_t stream);
+hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
+                        int64_t sTaub, float* T, int64_t sTb, int64_t ldt, int batch,
+                        hipStream_t stream);
+}  // namespace qr
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+constexpr int kMaxN = 4096;
+constexpr int kSmallN = 64;
+constexpr int kPanel = 16;
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+// Workspace of the blocked route: per-matrix T (16 x 16) then W2 (16 x n).
+size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kPanel * kPanel * sizeof(float)); }
+size_t ws_w_bytes(int batch, int n) {
+  return align_up((size_t)batch * kPanel * (size_t)n * sizeof(float));
+}
+
+int to_status(hipError_t e) { return e == hipSuccess ? QR_OK : QR_ELAUNCH; }
+
+// ---------------------------------------------------------------- tracing --
+// When a kernel's bit is set in the trace mask, each of its launches is
+// bracketed by two HIP events on the launch stream, and the launch's
+// algorithmic flops and bytes are recorded next to them.
+struct TraceRec {
+  hipEvent_t start;
+  hipEvent_t stop;
+  int kernel;
+  double flops;
+  double bytes;
+};
+
+std::mutex g_trace_mu;
+unsigned g_trace_mask = 0;
+std::vector<TraceRec> g_trace;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t pool_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Runs `launch` on `s`, traced if `kernel` is enabled.
+template <typename F>
+hipError_t traced(int kernel, double flops, double bytes, hipStream_t s, F&& launch) {
+  unsigned mask;
+  {
+    std::lock_guard<std::mutex> lk(g_trace_mu);
+    mask = g_trace_mask;
+  }
+  if (!(mask & (1u << kernel))) return launch();
+  hipEvent_t a, b;
+  {
+    std::lock_guard<std::mutex> lk(g_trace_mu);
+    a = pool_event();
+    b = pool_event();
+  }
+  if (!a || !b) return launch();
+  hipEventRecord(a, s);
+  const hipError_t e = launch();
+  hipEventRecord(b, s);
+  std::lock_guard<std::mutex> lk(g_trace_mu);
+  g_trace.push_back({a, b, kernel, flops, bytes});
+  return e;
+}
+
+// Algorithmic work per launch (whole batch), used for roofline figures.
+double panel_flops(int r, int kw) {  // sgeqr2 on r x kw + the T recurrence
+  return 2.0 * r * kw * kw - 2.0 / 3.0 * kw * kw * kw + 1.0 / 3.0 * kw * kw * kw;
+}
+
+// Highest element offset (+1) touched by a (batch, n, n) view with these strides.
+bool extent(int batch, int n, int64_t sb, int64_t sr, int64_t sc, int64_t* out) {
+  if (sb < 0 || sr < 0 || sc < 0) return false;
+  *out = (int64_t)(batch - 1) * sb + (int64_t)(n - 1) * sr + (int64_t)(n - 1) * sc + 1;
+  return true;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  const char* pa = static_cast<const char*>(a);
+  const char* pb = static_cast<const char*>(b);
+  return pa < pb + bbytes && pb < pa + abytes;
+}
+
+int check_geqrf_args(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, const float* H,
+                     const float* tau, int batch, int n) {
+  if (batch < 0 || n < 0) return QR_EINVAL;
+  if (n > kMaxN) return QR_EUNSUPPORTED;
+  if (batch == 0 || n == 0) return QR_OK;
+  if (!A || !H || !tau) return QR_EINVAL;
+  int64_t ext = 0;
+  if (!extent(batch, n, sAb, sAr, sAc, &ext)) return QR_EINVAL;
+  const size_t hbytes = (size_t)batch * n * n * sizeof(float);
+  const size_t tbytes = (size_t)batch * n * sizeof(float);
+  if (overlaps(A, (size_t)ext * sizeof(float), H, hbytes)) return QR_EINVAL;
+  if (overlaps(A, (size_t)ext * sizeof(float), tau, tbytes)) return QR_EINVAL;
+  if (overlaps(H, hbytes, tau, tbytes)) return QR_EINVAL;
+  return QR_OK;
+}
+
+hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
+                      int batch, int n, hipStream_t s) {
+  const double flops = 4.0 / 3.0 * n * n * (double)n * batch;
+  const double bytes = (2.0 * n * n + n) * 4.0 * batch;
+  return traced(QR_KERNEL_SMALLN, flops, bytes, s, [&] {
+    return qr::launch_geqrf_smalln(A, sAb, sAr, sAc, H, (int64_t)n * n, tau, n, batch, n, s);
+  });
+}
+
+hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
+                     int64_t sTaub, float* T, int batch, hipStream_t s) {
+  const double flops = panel_flops(r, kw) * batch;
+  const double bytes = (2.0 * r * kw + kw + kPanel * kPanel) * 4.0 * batch;
+  return traced(QR_KERNEL_PANEL, flops, bytes, s, [&] {
+    return qr::launch_panel16(H, sHb, ldh, j0, r, kw, tau, sTaub, T, kPanel * kPanel, batch, s);
+  });
+}
+
+hipError_t run_wy(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c, const float* T,
+                  int64_t sTb, float* W2, int64_t sWb, int batch, hipStream_t s) {
+  const double k = kPanel;
+  hipError_t e = traced(QR_KERNEL_WY_W2, (2.0 * r * k * c + k * k * c) * batch,
+                        ((double)r * c + r * k + k * c + k * k) * 4.0 * batch, s, [&] {
+                          return qr::launch_wy_w2_16(H, sHb, ldh, j0, r, c, T, sTb, W2, sWb,
+                                                     batch, s);
+                        });
+  if (e != hipSuccess) return e;
+  return traced(QR_KERNEL_WY_APPLY, 2.0 * r * k * c * batch,
+                (2.0 * r * c + r * k + k * c) * 4.0 * batch, s, [&] {
+                  return qr::launch_wy_apply_16(H, sHb, ldh, j0, r, c, W2, sWb, batch, s);
+                });
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qr_status_string(int status) {
+  switch (status) {
+    case QR_OK: return "ok";
+    case QR_EINVAL: return "invalid argument";
+    case QR_EUNSUPPORTED: return "unsupported matrix size";
+    case QR_EWORKSPACE: return "workspace too small";
+    case QR_ELAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int qr_abi_version(void) { return kAbiVersion; }
+
+int qr_max_n(void) { return kMaxN; }
+
+size_t qr_geqrf_f32_workspace(int batch, int n) {
+  if (batch <= 0 || n <= kSmallN || n > kMaxN) return 0;
+  return ws_t_bytes(batch) + ws_w_bytes(batch, n);
+}
+
+int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                        float* tau, int batch, int n, void* stream) {
+  int st = check_geqrf_args(A, sAb, sAr, sAc, H, tau, batch, n);
+  if (st != QR_OK || batch == 0 || n == 0) return st;
+  if (n > kSmallN) return QR_EUNSUPPORTED;
+  return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, static_cast<hipStream_t>(stream)));
+}
+
+int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
+                 int batch, int n, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_geqrf_args(A, sAb, sAr, sAc, H, tau, batch, n);
+  if (st != QR_OK || batch == 0 || n == 0) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nn = (int64_t)n * n;
+  if (n <= kSmallN) return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s));
+
+  const size_t need = qr_geqrf_f32_workspace(batch, n);
+  if (workspace_bytes < need || !workspace) return QR_EWORKSPACE;
+  float* Tws = static_cast<float*>(workspace);
+  float* Wws = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws_t_bytes(batch));
+
+  hipError_t e = traced(QR_KERNEL_COPY, 0.0, 2.0 * nn * 4.0 * batch, s, [&] {
+    return qr::launch_copy_in(A, sAb, sAr, sAc, H, nn, batch, n, s);
+  });
+  if (e != hipSuccess) return QR_ELAUNCH;
+  for (int j0 = 0; j0 < n; j0 += kPanel) {
+    const int kw = (n - j0) < kPanel ? (n - j0) : kPanel;
+    const int r = n - j0;
+    const int c = n - j0 - kw;
+    e = run_panel(H, nn, n, j0, r, kw, tau, n, Tws, batch, s);
+    if (e != hipSuccess) return QR_ELAUNCH;
+    if (c > 0) {
+      e = run_wy(H, nn, n, j0, r, c, Tws, kPanel * kPanel, Wws, (int64_t)kPanel * n, batch, s);
+      if (e != hipSuccess) return QR_ELAUNCH;
+    }
+  }
+  return QR_OK;
+}
+
+int qr_panel_f32(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
+                 int64_t sTaub, float* T, int64_t sTb, int batch, void* stream) {
+  if (batch < 0 || j0 < 0 || r < 0 || kw < 0 || sHb < 0 || sTaub < 0 || sTb < 0) return QR_EINVAL;
+  if (batch == 0 || r == 0 || kw == 0) return QR_OK;
+  if (!H || !tau || !T) return QR_EINVAL;
+  if (kw > kPanel || r < kw || ldh < j0 + kw) return QR_EINVAL;
+  if (r > kMaxN) return QR_EUNSUPPORTED;
+  if (sTb < kPanel * kPanel) return QR_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return to_status(traced(QR_KERNEL_PANEL, panel_flops(r, kw) * batch,
+                          (2.0 * r * kw + kw + kPanel * kPanel) * 4.0 * batch, s, [&] {
+                            return qr::launch_panel16(H, sHb, ldh, j0, r, kw, tau, sTaub, T, sTb,
+                                                      batch, s);
+                          }));
+}
+
+int qr_larft_f32(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
+                 int64_t sTaub, float* T, int64_t sTb, int64_t ldt, int batch, void* stream) {
+  if (batch < 0 || m < 0 || k < 0 || sVb < 0 || sTaub < 0 || sTb < 0) return QR_EINVAL;
+  if (batch == 0 || k == 0) return QR_OK;
+  if (!V || !tau || !T) return QR_EINVAL;
+  if (k > 64) return QR_EUNSUPPORTED;
+  if (m < k || ldv < k || ldt < k || sTb < (int64_t)(k - 1) * ldt + k) return QR_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const double flops = ((double)m * k * k + k * k * (double)k / 3.0) * batch;
+  return to_status(traced(QR_KERNEL_LARFT, flops, ((double)m * k + k + k * k) * 4.0 * batch, s,
+                          [&] {
+                            return qr::launch_larft(V, sVb, ldv, m, k, tau, sTaub, T, sTb, ldt,
+                                                    batch, s);
+                          }));
+}
+
+int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c, const float* T,
+                     int64_t sTb, void* workspace, size_t workspace_bytes, int batch,
+                     void* stream) {
+  if (batch < 0 || j0 < 0 || r < 0 || c < 0 || sHb < 0 || sTb < 0) return QR_EINVAL;
+  if (batch == 0 || r == 0 || c == 0) return QR_OK;
+  if (!H || !T) return QR_EINVAL;
+  if (r < kPanel || ldh < j0 + kPanel + c || sTb < kPanel * kPanel) return QR_EINVAL;
+  const size_t need = (size_t)batch * kPanel * (size_t)c * sizeof(float);
+  if (!workspace || workspace_bytes < need) return QR_EWORKSPACE;
+  return to_status(run_wy(H, sHb, ldh, j0, r, c, T, sTb, static_cast<float*>(workspace),
+                          (int64_t)kPanel * c, batch, static_cast<hipStream_t>(stream)));
+}
+
+int qr_trace_enable(unsigned kernel_mask) {
+  std::lock_guard<std::mutex> lk(g_trace_mu);
+  g_trace_mask = kernel_mask;
+  return QR_OK;
+}
+
+int qr_trace_reset(void) {
+  std::lock_guard<std::mutex> lk(g_trace_mu);
+  for (auto& t : g_trace) {
+    g_event_pool.push_back(t.start);
+    g_event_pool.push_back(t.stop);
+  }
+  g_trace.clear();
+  return QR_OK;
+}
+
+int qr_trace_read(int kernel, int* launches, double* total_ms, double* flops, double* bytes) {
+  if (!launches || !total_ms || !flops || !bytes) return QR_EINVAL;
+  std::lock_guard<std::mutex> lk(g_trace_mu);
+  int cnt = 0;
+  double ms = 0.0, fl = 0.0, by = 0.0;
+  for (auto& t : g_trace) {
+    if (t.kernel != kernel) continue;
+    if (hipEventSynchronize(t.stop) != hipSuccess) return QR_ELAUNCH;
+    float dt = 0.0f;
+    if (hipEventElapsedTime(&dt, t.start, t.stop) != hipSuccess) return QR_ELAUNCH;
+    ++cnt;
+    ms += dt;
+    fl += t.flops;
+    by += t.bytes;
+  }
+  *launches = cnt;
+  *total_ms = ms;
+  *flops = fl;
+  *bytes = by;
+  return QR_OK;
+}
+
+}  // extern "C"

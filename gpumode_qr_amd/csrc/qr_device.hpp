@@ -1,0 +1,155 @@
+// qr_device.hpp -- device helpers shared by the gfx950 QR kernels.
+//
+// Reflector convention (reference: src/qrbench/triton_kernels.py:686-700, made
+// LAPACK-slarfg exact): for the column [alpha; x],
+//   beta  = -sign(alpha) * hypot(alpha, ||x||),
+//   tau   = (beta - alpha) / beta,
+//   v     = [1; (x * pre) * gamma],  gamma = 1 / (alpha_s - beta_s),
+// and ||x|| == 0 gives tau = 0, beta = alpha with x left untouched. `pre` is the
+// power-of-two rescale of slarfg's |beta| < safmin loop (1 on the fast path).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace qr {
+
+// LAPACK slamch('S') / slamch('E') = 2^-126 / 2^-24.
+constexpr float kSafmin = 0x1p-102f;
+constexpr float kRsafmn = 0x1p102f;
+// Fast path is taken when sigma = sum(x^2) was computed without over/underflow
+// damage and alpha^2 cannot overflow; then ||x|| = sqrt(sigma) and
+// |beta| >= 2^-50 > safmin, so slarfg's rescale loop cannot trigger.
+constexpr float kSigmaLo = 0x1p-100f;
+constexpr float kSigmaHi = 0x1p100f;
+constexpr float kAlphaHi = 0x1p50f;
+
+struct Reflector {
+  float beta;   // new diagonal entry R[j][j]
+  float tau;    // reflector coefficient
+  float gamma;  // v = (x * pre) * gamma below the diagonal
+  float pre;    // power-of-two prescale (1 unless slarfg rescaled)
+};
+
+__device__ __forceinline__ bool reflector_fast_ok(float alpha, float sigma) {
+  return sigma >= kSigmaLo && sigma <= kSigmaHi && fabsf(alpha) <= kAlphaHi;
+}
+
+// Fast path: sigma = sum(x^2) in [2^-100, 2^100], |alpha| <= 2^50.
+__device__ __forceinline__ Reflector reflector_fast(float alpha, float sigma) {
+  Reflector r;
+  const float norm = sqrtf(fmaf(alpha, alpha, sigma));
+  const float beta = -copysignf(norm, alpha);
+  r.beta = beta;
+  r.tau = (beta - alpha) / beta;
+  r.gamma = 1.0f / (alpha - beta);
+  r.pre = 1.0f;
+  return r;
+}
+
+// LAPACK slapy2: sqrt(x^2 + y^2) without destructive over/underflow.
+__device__ __forceinline__ float lapy2(float x, float y) {
+  const float xa = fabsf(x), ya = fabsf(y);
+  const float w = fmaxf(xa, ya), z = fminf(xa, ya);
+  if (z == 0.0f || w > 3.402823466e38f) return w;
+  const float q = z / w;
+  return w * sqrtf(1.0f + q * q);
+}
+
+// General path from the scaled norm ||x|| = xmax * sqrt(ssq), where
+// ssq = sum((x_i / xmax)^2). Implements slarfg's branches exactly: zero norm,
+// the |beta| < safmin rescale loop (at most one pass is ever needed in fp32,
+// since |beta| >= 2^-149 and 2^-149 * 2^102 > safmin) and the final unscale.
+__device__ __forceinline__ Reflector reflector_scaled(float alpha, float xmax, float ssq) {
+  Reflector r;
+  const float rt = sqrtf(ssq);
+  const float xnorm = xmax * rt;
+  if (xnorm == 0.0f) {
+    r.beta = alpha;
+    r.tau = 0.0f;
+    r.gamma = 1.0f;
+    r.pre = 1.0f;
+    return r;
+  }
+  float beta = -copysignf(lapy2(alpha, xnorm), alpha);
+  float a = alpha;
+  float pre = 1.0f;
+  int knt = 0;
+  while (fabsf(beta) < kSafmin && knt < 20) {
+    ++knt;
+    pre *= kRsafmn;
+    beta *= kRsafmn;
+    a *= kRsafmn;
+  }
+  if (knt > 0) {
+    const float xn = (xmax * pre) * rt;
+    beta = -copysignf(lapy2(a, xn), a);
+  }
+  r.tau = (beta - a) / beta;
+  r.gamma = 1.0f / (a - beta);
+  for (int i = 0; i < knt; ++i) beta *= kSafmin;
+  r.beta = beta;
+  r.pre = pre;
+  return r;
+}
+
+// Reflector that leaves everything unchanged (no rows below the diagonal).
+__device__ __forceinline__ Reflector reflector_identity(float alpha) {
+  Reflector r;
+  r.beta = alpha;
+  r.tau = 0.0f;
+  r.gamma = 1.0f;
+  r.pre = 1.0f;
+  return r;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Broadcast lane J of each 16-lane DPP row to the whole row (gfx90a+ row_newbcast).
+template <int J>
+__device__ __forceinline__ float row_bcast16(float v) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, false));
+}
+
+// Same broadcast as a volatile asm: the compiler may not merge two uses into
+// one live register, so hot loops can re-broadcast instead of holding a copy.
+template <int J>
+__device__ __forceinline__ float row_bcast16_nocse(float v) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  float out;
+  asm volatile("v_mov_b32_dpp %0, %1 row_newbcast:%2 row_mask:0xf bank_mask:0xf"
+               : "=v"(out)
+               : "v"(v), "i"(J));
+  return out;
+}
+
+// Sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float sum_over_rows16(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ float max_over_rows16(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+}  // namespace qr

@@ -1,0 +1,143 @@
+"""Torch-facing wrappers of the gfx950 QR kernels.
+
+``geqrf(A) -> (H, tau)`` is the drop-in forward pass: same contract as
+``torch.geqrf`` and the reference's variants (src/qrbench/reference.py:15-20,
+src/qrbench/variants.py:102): ``A`` is ``(batch, n, n)`` float32 on a GPU and is
+not modified; ``H`` (row-major contiguous) holds R on and above the diagonal and
+the essential Householder vectors below it; ``tau`` is ``(batch, n)``. All work
+is enqueued on torch's current stream of ``A``'s device; nothing synchronises.
+
+The other functions expose the individual kernels (panel, larft, WY update) for
+the parity tests. Torch is only used for device memory and the stream.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+PANEL = 16  # panel width of the blocked route
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_input(A: torch.Tensor) -> None:
+    if not isinstance(A, torch.Tensor):
+        raise TypeError("A must be a torch.Tensor")
+    if A.dim() != 3 or A.shape[-1] != A.shape[-2]:
+        raise ValueError(f"A must be (batch, n, n); got {tuple(A.shape)}")
+    if A.dtype != torch.float32:
+        raise TypeError(f"A must be float32; got {A.dtype}")
+    if A.device.type != "cuda":
+        raise ValueError("A must be on a GPU device (the HIP path has no CPU fallback)")
+
+
+def workspace_bytes(batch: int, n: int) -> int:
+    return int(_lib.load().qr_geqrf_f32_workspace(batch, n))
+
+
+def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None):
+    """Batched compact-Householder QR on the GPU: ``(H, tau)`` like torch.geqrf."""
+    _check_input(A)
+    lib = _lib.load()
+    b, n, _ = A.shape
+    dev = A.device
+    H = torch.empty((b, n, n), dtype=torch.float32, device=dev)
+    tau = torch.empty((b, n), dtype=torch.float32, device=dev)
+    if b == 0 or n == 0:
+        return H, tau
+    need = int(lib.qr_geqrf_f32_workspace(b, n))
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws_ptr, ws_len = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    else:
+        ws_ptr, ws_len = None, 0
+    sb, sr, sc = A.stride()
+    with torch.cuda.device(dev):
+        st = lib.qr_geqrf_f32(
+            A.data_ptr(), sb, sr, sc, H.data_ptr(), tau.data_ptr(), b, n, ws_ptr, ws_len,
+            _stream(dev),
+        )
+    _lib.check("qr_geqrf_f32", st)
+    return H, tau
+
+
+def fused_smalln(A: torch.Tensor):
+    """Kernel (a) alone: n <= 64, one wavefront per matrix."""
+    _check_input(A)
+    lib = _lib.load()
+    b, n, _ = A.shape
+    H = torch.empty((b, n, n), dtype=torch.float32, device=A.device)
+    tau = torch.empty((b, n), dtype=torch.float32, device=A.device)
+    sb, sr, sc = A.stride()
+    with torch.cuda.device(A.device):
+        st = lib.qr_fused_smalln_f32(
+            A.data_ptr(), sb, sr, sc, H.data_ptr(), tau.data_ptr(), b, n, _stream(A.device)
+        )
+    _lib.check("qr_fused_smalln_f32", st)
+    return H, tau
+
+
+def panel(P: torch.Tensor):
+    """Kernel (b) alone on a batch of (r, kw) panels (kw <= 16).
+
+    Returns ``(H_p, tau, T)``: the factored panel in geqrf packing, its ``kw``
+    reflector coefficients and the 16 x 16 compact-WY factor (upper, zero
+    beyond ``kw``), like the reference's ``hh_panel_qr`` minus the explicit V
+    (src/qrbench/triton_kernels.py:912-967).
+    """
+    if P.dim() != 3 or P.dtype != torch.float32 or P.device.type != "cuda":
+        raise ValueError("P must be a (batch, r, kw) float32 GPU tensor")
+    lib = _lib.load()
+    b, r, kw = P.shape
+    Hp = P.contiguous().clone()
+    tau = torch.zeros((b, kw), dtype=torch.float32, device=P.device)
+    T = torch.empty((b, PANEL, PANEL), dtype=torch.float32, device=P.device)
+    with torch.cuda.device(P.device):
+        st = lib.qr_panel_f32(
+            Hp.data_ptr(), r * kw, kw, 0, r, kw, tau.data_ptr(), kw, T.data_ptr(), PANEL * PANEL,
+            b, _stream(P.device),
+        )
+    _lib.check("qr_panel_f32", st)
+    return Hp, tau, T
+
+
+def larft(V: torch.Tensor, tau: torch.Tensor):
+    """Kernel (c) alone: T (k x k) of reflectors stored below the diagonal of V."""
+    if V.dim() != 3 or tau.dim() != 2:
+        raise ValueError("V must be (batch, m, k) and tau (batch, k)")
+    lib = _lib.load()
+    b, m, k = V.shape
+    Vc = V.contiguous()
+    tc = tau.contiguous()
+    T = torch.empty((b, k, k), dtype=torch.float32, device=V.device)
+    with torch.cuda.device(V.device):
+        st = lib.qr_larft_f32(
+            Vc.data_ptr(), m * k, k, m, k, tc.data_ptr(), k, T.data_ptr(), k * k, k, b,
+            _stream(V.device),
+        )
+    _lib.check("qr_larft_f32", st)
+    return T
+
+
+def wy_update(Hpanel: torch.Tensor, T: torch.Tensor):
+    """Kernel (d) alone: given a (batch, r, 16 + c) block whose first 16 columns
+    hold a factored panel (V below the diagonal) and T (batch, 16, 16), return a
+    copy with the last c columns replaced by C - V T^T V^T C."""
+    lib = _lib.load()
+    b, r, width = Hpanel.shape
+    c = width - PANEL
+    out = Hpanel.contiguous().clone()
+    Tc = T.contiguous()
+    ws = torch.empty(max(1, b * PANEL * c * 4), dtype=torch.uint8, device=Hpanel.device)
+    with torch.cuda.device(Hpanel.device):
+        st = lib.qr_wy_update_f32(
+            out.data_ptr(), r * width, width, 0, r, c, Tc.data_ptr(), PANEL * PANEL,
+            ws.data_ptr(), ws.numel(), b, _stream(Hpanel.device),
+        )
+    _lib.check("qr_wy_update_f32", st)
+    return out

@@ -1,0 +1,249 @@
+"""Parity of the gfx950 HIP path against the CPU oracle, through the C ABI.
+
+Each test prints its case before touching the GPU so a failing run names it.
+Tolerance (tests/parity.py): |dV|, |dtau|, |dR|/||A[:,j]||_2 <= 4 n eps32 on
+well-conditioned inputs; rank-deficient and cond-1e6 inputs are gates-only.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpumode_qr_amd import checker, hip_qr, inputs
+from tests.parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _say(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _gauss(batch, n, seed, cond=0.0):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(batch, n, n, generator=g)
+    if cond:
+        A = A * torch.logspace(0, -cond, n)
+    return A
+
+
+def _run(A_cpu):
+    H, tau = hip_qr.geqrf(A_cpu.to(DEV))
+    torch.cuda.synchronize()
+    return H.cpu(), tau.cpu()
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 8, 17, 32, 33, 48, 63, 64])
+@pytest.mark.parametrize("batch", [1, 5])
+def test_fused_smalln_vs_oracle(oracle, n, batch):
+    _say(f"fused_smalln n={n} batch={batch}")
+    A = _gauss(batch, n, seed=100 + n + batch)
+    H, tau = hip_qr.fused_smalln(A.to(DEV))
+    torch.cuda.synchronize()
+    H, tau = H.cpu().numpy(), tau.cpu().numpy()
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H, tau, H_ref, tau_ref, what=f"smalln n={n}")
+    assert np.all(tau[:, -1] == 0.0)
+
+
+def test_fused_smalln_strided_input(oracle):
+    _say("fused_smalln strided (transposed) input n=40")
+    A = _gauss(3, 40, seed=7)
+    At = A.transpose(1, 2).contiguous().transpose(1, 2)  # same values, column-major strides
+    assert not At.is_contiguous()
+    H, tau = hip_qr.geqrf(At.to(DEV))
+    torch.cuda.synchronize()
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref)
+
+
+@pytest.mark.parametrize("r,kw", [(16, 16), (17, 16), (40, 16), (64, 16), (100, 16), (256, 16),
+                                  (300, 16), (777, 16), (1024, 16), (2048, 16), (2049, 16),
+                                  (3000, 16), (64, 5), (20, 13)])
+def test_panel_vs_oracle(oracle, r, kw):
+    _say(f"panel r={r} kw={kw}")
+    g = torch.Generator().manual_seed(r * 31 + kw)
+    P = torch.randn(3, r, kw, generator=g)
+    Hp, tau, T = hip_qr.panel(P.to(DEV))
+    torch.cuda.synchronize()
+    Hp, tau, T = Hp.cpu().numpy(), tau.cpu().numpy(), T.cpu().numpy()
+    for b in range(3):
+        Hr, tr = oracle.geqr2(P[b].numpy())
+        Tr = oracle.larft(Hr, tr)
+        tol = 4 * r * 2**-23
+        colnorm = np.linalg.norm(P[b].numpy().astype(np.float64), axis=0)
+        up = np.triu(np.ones((r, kw), bool))
+        dH = np.abs(Hp[b].astype(np.float64) - Hr)
+        assert (np.where(up, dH / colnorm, 0)).max() <= tol, "R"
+        assert (np.where(~up, dH, 0)).max() <= tol, "V"
+        assert np.abs(tau[b] - tr).max() <= tol, "tau"
+        assert np.abs(T[b, :kw, :kw] - Tr).max() <= 4 * tol, "T"
+        assert np.all(T[b, kw:, :] == 0) and np.all(T[b, :, kw:] == 0)
+
+
+@pytest.mark.parametrize("m,k", [(16, 16), (64, 16), (300, 32), (1000, 64), (40, 7)])
+def test_larft_vs_oracle(oracle, m, k):
+    _say(f"larft m={m} k={k}")
+    g = torch.Generator().manual_seed(m + k)
+    P = torch.randn(2, m, k, generator=g)
+    Vs, taus, Trefs = [], [], []
+    for b in range(2):
+        Hr, tr = oracle.geqr2(P[b].numpy())
+        Vs.append(Hr)
+        taus.append(tr)
+        Trefs.append(oracle.larft(Hr, tr))
+    V = torch.from_numpy(np.stack(Vs)).to(DEV)
+    tau = torch.from_numpy(np.stack(taus)).to(DEV)
+    T = hip_qr.larft(V, tau)
+    torch.cuda.synchronize()
+    T = T.cpu().numpy()
+    for b in range(2):
+        assert np.abs(T[b] - Trefs[b]).max() <= 16 * m * 2**-23
+
+
+@pytest.mark.parametrize("r,c", [(16, 1), (64, 48), (100, 77), (512, 496), (1030, 200)])
+def test_wy_update_vs_oracle(oracle, r, c):
+    _say(f"wy_update r={r} c={c}")
+    g = torch.Generator().manual_seed(r + 3 * c)
+    P = torch.randn(2, r, 16, generator=g)
+    C = torch.randn(2, r, c, generator=g)
+    blocks, Ts, refs = [], [], []
+    for b in range(2):
+        Hr, tr = oracle.geqr2(P[b].numpy())
+        Tr = oracle.larft(Hr, tr)
+        T16 = np.zeros((16, 16), np.float32)
+        T16[:16, :16] = Tr
+        Ts.append(T16)
+        blocks.append(np.concatenate([Hr, C[b].numpy()], axis=1))
+        refs.append(oracle.larfb_lt(Hr, Tr, C[b].numpy()))
+    blk = torch.from_numpy(np.stack(blocks)).to(DEV)
+    T = torch.from_numpy(np.stack(Ts)).to(DEV)
+    out = hip_qr.wy_update(blk, T)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for b in range(2):
+        assert np.array_equal(out[b, :, :16], blocks[b][:, :16])  # V untouched
+        scale = max(1.0, float(np.abs(C[b].numpy()).max()))
+        assert np.abs(out[b, :, 16:] - refs[b]).max() <= 16 * r * 2**-23 * scale
+
+
+@pytest.mark.parametrize("n", [65, 80, 96, 128, 129, 176, 200, 352, 512])
+def test_geqrf_blocked_vs_oracle(oracle, n):
+    _say(f"geqrf blocked n={n}")
+    A = _gauss(3, n, seed=n)
+    H, tau = _run(A)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"n={n}")
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+
+
+def test_geqrf_matches_mkl_golden_fixtures():
+    from tests.test_oracle import _golden
+
+    for name, (A, H_ref, tau_ref) in _golden().items():
+        if name == "rank1_n16":
+            continue
+        _say(f"golden {name}")
+        H, tau = _run(torch.from_numpy(A))
+        assert_parity(A, H.numpy(), tau.numpy(), H_ref, tau_ref, what=name)
+
+
+@pytest.mark.parametrize("n", [24, 100])
+def test_geqrf_known_answers(n):
+    _say(f"known answers n={n}")
+    g = torch.Generator().manual_seed(n)
+    U = torch.triu(torch.randn(2, n, n, generator=g))
+    H, tau = _run(U)
+    assert torch.equal(H, U) and torch.all(tau == 0)
+    A = torch.randn(2, n, n, generator=g)
+    A[:, :, n // 3] = 0.0
+    H, tau = _run(A)
+    assert torch.all(tau[:, n // 3] == 0) and torch.all(H[:, n // 3, n // 3] == 0)
+    assert torch.all(tau[:, -1] == 0)
+
+
+@pytest.mark.parametrize("n", [32, 176, 512])
+def test_stress_suite_gates(n):
+    for prob in inputs.stress_cases(n=n, batch=4, device="cpu"):
+        _say(f"stress {prob.name}")
+        H, tau = _run(prob.tensor)
+        res = checker.check(prob.tensor, H, tau)
+        assert res.passed, (prob.name, res.as_dict())
+
+
+def test_config1_parity_and_gates(oracle):
+    _say("config 1 (b64 n32)")
+    A = inputs.config_tensor(inputs.CONFIGS[0])
+    H, tau = _run(A)
+    assert checker.check(A, H, tau).passed
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref)
+    Hm, tm = torch.geqrf(A)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), Hm.numpy(), tm.numpy(), what="vs MKL")
+
+
+def test_config2_parity_and_gates(oracle):
+    _say("config 2 (b2048 n64)")
+    A = inputs.config_tensor(inputs.CONFIGS[1])
+    H, tau = _run(A)
+    assert checker.check(A, H, tau).passed
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref)
+
+
+def test_config4_gates_and_sampled_parity(oracle):
+    _say("config 4 (b64 n1024)")
+    A = inputs.config_tensor(inputs.CONFIGS[3])
+    H, tau = _run(A)
+    assert checker.check(A, H, tau).passed
+    idx = [0, 37]
+    H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
+    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref)
+
+
+def test_config5_gates_and_gaussian_half_parity(oracle):
+    _say("config 5 (b16 n2048)")
+    A = inputs.config_tensor(inputs.CONFIGS[4])
+    H, tau = _run(A)
+    assert torch.isfinite(H).all() and torch.isfinite(tau).all()
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+    n = A.shape[-1]
+    assert torch.all(tau[8:, n // 3] == 0)  # zeroed column -> identity reflector
+    idx = [8, 15]
+    H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
+    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref)
+
+
+def test_config3_gates_sampled():
+    _say("config 3 (b640 n512), first 64 matrices")
+    A = inputs.config_tensor(inputs.CONFIGS[2])[:64]
+    H, tau = _run(A)
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+
+
+def test_input_not_modified_and_repeatable():
+    _say("A unchanged, two calls bit-identical (n=300)")
+    A = _gauss(4, 300, seed=9).to(DEV)
+    A0 = A.clone()
+    H1, t1 = hip_qr.geqrf(A)
+    H2, t2 = hip_qr.geqrf(A)
+    torch.cuda.synchronize()
+    assert torch.equal(A, A0)
+    assert torch.equal(H1, H2) and torch.equal(t1, t2)
+
+
+def test_variant_registry_runs_hip_path():
+    from gpumode_qr_amd.variants import CHAMPION, VARIANTS
+
+    _say("registry champion call")
+    A = _gauss(2, 70, seed=1).to(DEV)
+    H, tau = VARIANTS[CHAMPION](A)
+    torch.cuda.synchronize()
+    assert checker.check(A, H, tau).passed

@@ -1,0 +1,84 @@
+"""The C-ABI library loads and exports every symbol include/*.h declares.
+
+No compute call is made here: argument-validation paths return before any HIP
+call, so these run without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from gpumode_qr_amd import _lib
+
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+
+
+def _declared_functions() -> set[str]:
+    names = set()
+    for hdr in INCLUDE.glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(qr_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from gpumode_qr_amd.csrc import build
+
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_symbols():
+    assert _declared_functions() == set(_lib.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+
+
+def test_abi_and_limits(lib):
+    assert lib.qr_abi_version() == _lib.ABI_VERSION
+    assert lib.qr_max_n() == 4096
+    assert lib.qr_status_string(0) == b"ok"
+    assert lib.qr_status_string(3) == b"workspace too small"
+    assert lib.qr_status_string(99) == b"unknown status"
+
+
+def test_workspace_query(lib):
+    assert lib.qr_geqrf_f32_workspace(64, 32) == 0  # fused route needs none
+    assert lib.qr_geqrf_f32_workspace(0, 512) == 0
+    ws = lib.qr_geqrf_f32_workspace(640, 512)
+    assert ws >= 640 * (16 * 16 + 16 * 512) * 4
+    assert ws % 256 == 0
+
+
+def test_argument_validation_without_launch(lib):
+    p = ctypes.c_void_p(0x1000)
+    h = ctypes.c_void_p(0x10000000)
+    t = ctypes.c_void_p(0x20000000)
+    # empty problems are a successful no-op
+    assert lib.qr_geqrf_f32(None, 0, 0, 0, None, None, 0, 8, None, 0, None) == 0
+    assert lib.qr_geqrf_f32(None, 0, 0, 0, None, None, 4, 0, None, 0, None) == 0
+    # negative sizes, too-large n, null pointers, negative strides
+    assert lib.qr_geqrf_f32(p, 1, 1, 1, h, t, -1, 8, None, 0, None) == 1
+    assert lib.qr_geqrf_f32(p, 1, 1, 1, h, t, 1, 5000, None, 0, None) == 2
+    assert lib.qr_geqrf_f32(None, 64, 8, 1, h, t, 1, 8, None, 0, None) == 1
+    assert lib.qr_geqrf_f32(p, -64, 8, 1, h, t, 1, 8, None, 0, None) == 1
+    # H overlapping A
+    assert lib.qr_geqrf_f32(h, 64, 8, 1, h, t, 1, 8, None, 0, None) == 1
+    # workspace missing for the blocked route
+    assert lib.qr_geqrf_f32(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, None) == 3
+    # kernel-level entry points
+    assert lib.qr_fused_smalln_f32(p, 100 * 100, 100, 1, h, t, 1, 100, None) == 2
+    assert lib.qr_panel_f32(h, 100, 10, 0, 10, 17, t, 17, t, 256, 1, None) == 1
+    assert lib.qr_larft_f32(h, 100, 70, 100, 70, t, 70, t, 4900, 70, 1, None) == 2
+    assert lib.qr_wy_update_f32(h, 1000, 50, 0, 20, 34, t, 256, None, 0, 1, None) == 3
