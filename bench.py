@@ -114,6 +114,13 @@ def run_config(cfg: int, steps: int, warmup: int, torch, trace_kernels) -> dict:
     print(f"[bench] {prob.name}: median {med:.4f} ms  {row['gflops']:.0f} GFLOP/s "
           f"({row['pct_fp32_peak']:.2f}% fp32 peak)  {row['hbm_gbs']:.0f} GB/s algorithmic",
           flush=True)
+    reps = max(1, min(steps, 5))
+    for kname, kv in kernels.items():
+        if kv["launches"]:
+            print(f"[bench]   {kname:>7}: {kv['ms'] / reps:8.3f} ms/step  "
+                  f"{kv['launches'] // reps:5d} launches/step  "
+                  f"{kv['flops'] / (kv['ms'] * 1e-3) / 1e12:7.2f} TFLOP/s  "
+                  f"{kv['bytes'] / (kv['ms'] * 1e-3) / 1e9:7.0f} GB/s", flush=True)
     del A, ws
     torch.cuda.empty_cache()
     return row
@@ -181,7 +188,7 @@ def main() -> int:
 
     _lib.load()
     cfgs = [int(c) for c in args.configs.split(",") if c.strip()]
-    trace_kernels = ["smalln", "panel", "wy_w2", "wy_apply", "copy"]
+    trace_kernels = ["smalln", "panel", "trail", "copy"]
     rows = [run_config(c, args.steps, args.warmup, torch, trace_kernels) for c in cfgs]
     gm = bench.geomean([r["median_ms"] for r in rows])
 

@@ -30,7 +30,7 @@ SIGNATURES: dict[str, tuple] = {
     "qr_fused_smalln_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr]),
     "qr_panel_f32": (
         _int,
-        [_ptr, _i64, _i64, _int, _int, _int, _ptr, _i64, _ptr, _i64, _int, _ptr],
+        [_ptr, _i64, _i64, _int, _int, _int, _int, _ptr, _i64, _ptr, _i64, _int, _ptr],
     ),
     "qr_larft_f32": (
         _int,
@@ -38,7 +38,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "qr_wy_update_f32": (
         _int,
-        [_ptr, _i64, _i64, _int, _int, _int, _ptr, _i64, _ptr, _size, _int, _ptr],
+        [_ptr, _i64, _i64, _int, _int, _int, _int, _ptr, _i64, _int, _ptr],
     ),
     "qr_trace_enable": (_int, [ctypes.c_uint]),
     "qr_trace_reset": (_int, []),
@@ -55,9 +55,9 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 # qr_kernel_id values of include/qr_gfx950.h
-KERNELS = {"smalln": 0, "panel": 1, "wy_w2": 2, "wy_apply": 3, "copy": 4, "larft": 5}
+KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4}
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 QR_OK = 0
 

@@ -4,14 +4,16 @@
 // Driver (reference: _hh_panel_blocked_qr, src/qrbench/variants.py:761-805, and
 // the n <= 128 fused route of make_hh_fused_smalln, :739-758):
 //   n <= 64 : one launch of the fused small-n kernel (A -> H directly).
-//   n >  64 : copy A -> H, then for each 16-wide panel at column j0:
-//             panel kernel (V and tau in place, T to the workspace), then the
-//             trailing update C -= V T^T V^T C on the columns to its right
-//             (W2 = T^T V^T C kernel, then the C -= V W2 kernel).
+//   n >  64 : copy A -> H, then for each outer block of P 16-wide panels at
+//             column J0: P panel launches (panel p first applies panels 0..p-1
+//             of the block to its columns, then factors them; V and tau in
+//             place, T_p to the workspace), then one trailing launch that
+//             applies the P block reflectors to every column right of the block.
 // Everything is enqueued on the caller's stream; nothing synchronises except
 // qr_trace_read, which waits for the events it reads.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -21,13 +23,11 @@ namespace qr {
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                                int64_t sHb, float* tau, int64_t sTb, int batch, int n,
                                hipStream_t stream);
-hipError_t launch_panel16(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
-                          int64_t sTaub, float* T, int64_t sTb, int batch, hipStream_t stream);
-hipError_t launch_wy_w2_16(const float* H, int64_t sHb, int64_t ldh, int j0, int r, int c,
-                           const float* T, int64_t sTb, float* W2, int64_t sWb, int batch,
-                           hipStream_t stream);
-hipError_t launch_wy_apply_16(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c,
-                              const float* W2, int64_t sWb, int batch, hipStream_t stream);
+hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
+                        float* tau, int64_t sTaub, float* Tws, int64_t sTwb, int batch,
+                        hipStream_t stream);
+hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
+                        int ncols, const float* Tws, int64_t sTwb, int batch, hipStream_t stream);
 hipError_t launch_copy_in(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                           int64_t sHb, int batch, int n, hipStream_t stream);
 hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
@@ -37,18 +37,28 @@ hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, 
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 constexpr int kMaxN = 4096;
 constexpr int kSmallN = 64;
 constexpr int kPanel = 16;
+constexpr int kMaxBlocks = 8;  // 16-wide panels per outer block
+constexpr int kTStride = kMaxBlocks * kPanel * kPanel;  // T floats per matrix
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
-// Workspace of the blocked route: per-matrix T (16 x 16) then W2 (16 x n).
-size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kPanel * kPanel * sizeof(float)); }
-size_t ws_w_bytes(int batch, int n) {
-  return align_up((size_t)batch * kPanel * (size_t)n * sizeof(float));
+// Workspace of the blocked route: per matrix, the 16 x 16 T of each panel of
+// the current outer block.
+size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kTStride * sizeof(float)); }
+
+// Panels per outer block for size n (QR_OUTER_BLOCKS=1..8 overrides).
+int outer_blocks(int n) {
+  if (const char* env = std::getenv("QR_OUTER_BLOCKS")) {
+    const int v = std::atoi(env);
+    if (v >= 1 && v <= kMaxBlocks) return v;
+  }
+  (void)n;
+  return 4;
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? QR_OK : QR_ELAUNCH; }
@@ -148,28 +158,24 @@ hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, flo
   });
 }
 
-hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
-                     int64_t sTaub, float* T, int batch, hipStream_t s) {
-  const double flops = panel_flops(r, kw) * batch;
-  const double bytes = (2.0 * r * kw + kw + kPanel * kPanel) * 4.0 * batch;
+hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw, float* tau,
+                     int64_t sTaub, float* T, int64_t sTb, int batch, hipStream_t s) {
+  // left-looking MFMA work (panels 0..p-1) + the panel's own factorisation
+  const double flops = (4.0 * r * kPanel * kPanel * p + panel_flops(r - 16 * p, kw)) * batch;
+  const double bytes = (2.0 * r * kw + (double)r * kPanel * p + kw + kPanel * kPanel * (p + 1)) *
+                       4.0 * batch;
   return traced(QR_KERNEL_PANEL, flops, bytes, s, [&] {
-    return qr::launch_panel16(H, sHb, ldh, j0, r, kw, tau, sTaub, T, kPanel * kPanel, batch, s);
+    return qr::launch_panel(H, sHb, ldh, J0, p, r, kw, tau, sTaub, T, sTb, batch, s);
   });
 }
 
-hipError_t run_wy(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c, const float* T,
-                  int64_t sTb, float* W2, int64_t sWb, int batch, hipStream_t s) {
-  const double k = kPanel;
-  hipError_t e = traced(QR_KERNEL_WY_W2, (2.0 * r * k * c + k * k * c) * batch,
-                        ((double)r * c + r * k + k * c + k * k) * 4.0 * batch, s, [&] {
-                          return qr::launch_wy_w2_16(H, sHb, ldh, j0, r, c, T, sTb, W2, sWb,
-                                                     batch, s);
-                        });
-  if (e != hipSuccess) return e;
-  return traced(QR_KERNEL_WY_APPLY, 2.0 * r * k * c * batch,
-                (2.0 * r * c + r * k + k * c) * 4.0 * batch, s, [&] {
-                  return qr::launch_wy_apply_16(H, sHb, ldh, j0, r, c, W2, sWb, batch, s);
-                });
+hipError_t run_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int ncols,
+                     const float* T, int64_t sTb, int batch, hipStream_t s) {
+  const double flops = 4.0 * r * kPanel * (double)ncols * nblk * batch;
+  const double bytes = (2.0 * r * ncols + (double)r * kPanel * nblk) * 4.0 * batch;
+  return traced(QR_KERNEL_TRAIL, flops, bytes, s, [&] {
+    return qr::launch_trail(H, sHb, ldh, J0, nblk, r, kPanel * nblk, ncols, T, sTb, batch, s);
+  });
 }
 
 }  // namespace
@@ -193,7 +199,7 @@ int qr_max_n(void) { return kMaxN; }
 
 size_t qr_geqrf_f32_workspace(int batch, int n) {
   if (batch <= 0 || n <= kSmallN || n > kMaxN) return 0;
-  return ws_t_bytes(batch) + ws_w_bytes(batch, n);
+  return ws_t_bytes(batch);
 }
 
 int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
@@ -215,40 +221,41 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   const size_t need = qr_geqrf_f32_workspace(batch, n);
   if (workspace_bytes < need || !workspace) return QR_EWORKSPACE;
   float* Tws = static_cast<float*>(workspace);
-  float* Wws = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws_t_bytes(batch));
 
   hipError_t e = traced(QR_KERNEL_COPY, 0.0, 2.0 * nn * 4.0 * batch, s, [&] {
     return qr::launch_copy_in(A, sAb, sAr, sAc, H, nn, batch, n, s);
   });
   if (e != hipSuccess) return QR_ELAUNCH;
-  for (int j0 = 0; j0 < n; j0 += kPanel) {
-    const int kw = (n - j0) < kPanel ? (n - j0) : kPanel;
-    const int r = n - j0;
-    const int c = n - j0 - kw;
-    e = run_panel(H, nn, n, j0, r, kw, tau, n, Tws, batch, s);
-    if (e != hipSuccess) return QR_ELAUNCH;
-    if (c > 0) {
-      e = run_wy(H, nn, n, j0, r, c, Tws, kPanel * kPanel, Wws, (int64_t)kPanel * n, batch, s);
+  const int P = outer_blocks(n);
+  for (int J0 = 0; J0 < n; J0 += kPanel * P) {
+    const int r = n - J0;
+    const int nblk = (r + kPanel - 1) / kPanel < P ? (r + kPanel - 1) / kPanel : P;
+    for (int p = 0; p < nblk; ++p) {
+      const int kw = (r - kPanel * p) < kPanel ? (r - kPanel * p) : kPanel;
+      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s);
+      if (e != hipSuccess) return QR_ELAUNCH;
+    }
+    const int ncols = r - kPanel * nblk;
+    if (ncols > 0) {
+      e = run_trail(H, nn, n, J0, nblk, r, ncols, Tws, kTStride, batch, s);
       if (e != hipSuccess) return QR_ELAUNCH;
     }
   }
   return QR_OK;
 }
 
-int qr_panel_f32(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
+int qr_panel_f32(float* H, int64_t sHb, int64_t ldh, int j0, int p, int r, int kw, float* tau,
                  int64_t sTaub, float* T, int64_t sTb, int batch, void* stream) {
-  if (batch < 0 || j0 < 0 || r < 0 || kw < 0 || sHb < 0 || sTaub < 0 || sTb < 0) return QR_EINVAL;
+  if (batch < 0 || j0 < 0 || p < 0 || r < 0 || kw < 0 || sHb < 0 || sTaub < 0 || sTb < 0)
+    return QR_EINVAL;
   if (batch == 0 || r == 0 || kw == 0) return QR_OK;
   if (!H || !tau || !T) return QR_EINVAL;
-  if (kw > kPanel || r < kw || ldh < j0 + kw) return QR_EINVAL;
+  if (kw > kPanel || p >= kMaxBlocks || r < kPanel * p + kw || ldh < j0 + kPanel * p + kw)
+    return QR_EINVAL;
   if (r > kMaxN) return QR_EUNSUPPORTED;
-  if (sTb < kPanel * kPanel) return QR_EINVAL;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return to_status(traced(QR_KERNEL_PANEL, panel_flops(r, kw) * batch,
-                          (2.0 * r * kw + kw + kPanel * kPanel) * 4.0 * batch, s, [&] {
-                            return qr::launch_panel16(H, sHb, ldh, j0, r, kw, tau, sTaub, T, sTb,
-                                                      batch, s);
-                          }));
+  if (sTb < (int64_t)kPanel * kPanel * (p + 1)) return QR_EINVAL;
+  return to_status(
+      run_panel(H, sHb, ldh, j0, p, r, kw, tau, sTaub, T, sTb, batch, static_cast<hipStream_t>(stream)));
 }
 
 int qr_larft_f32(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
@@ -267,17 +274,17 @@ int qr_larft_f32(const float* V, int64_t sVb, int64_t ldv, int m, int k, const f
                           }));
 }
 
-int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c, const float* T,
-                     int64_t sTb, void* workspace, size_t workspace_bytes, int batch,
-                     void* stream) {
-  if (batch < 0 || j0 < 0 || r < 0 || c < 0 || sHb < 0 || sTb < 0) return QR_EINVAL;
-  if (batch == 0 || r == 0 || c == 0) return QR_OK;
+int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int nblk, int r, int c,
+                     const float* T, int64_t sTb, int batch, void* stream) {
+  if (batch < 0 || j0 < 0 || nblk < 0 || r < 0 || c < 0 || sHb < 0 || sTb < 0) return QR_EINVAL;
+  if (batch == 0 || r == 0 || c == 0 || nblk == 0) return QR_OK;
   if (!H || !T) return QR_EINVAL;
-  if (r < kPanel || ldh < j0 + kPanel + c || sTb < kPanel * kPanel) return QR_EINVAL;
-  const size_t need = (size_t)batch * kPanel * (size_t)c * sizeof(float);
-  if (!workspace || workspace_bytes < need) return QR_EWORKSPACE;
-  return to_status(run_wy(H, sHb, ldh, j0, r, c, T, sTb, static_cast<float*>(workspace),
-                          (int64_t)kPanel * c, batch, static_cast<hipStream_t>(stream)));
+  if (nblk > kMaxBlocks || r < kPanel * (nblk - 1) + 1 || ldh < j0 + kPanel * nblk + c ||
+      sTb < (int64_t)kPanel * kPanel * nblk)
+    return QR_EINVAL;
+  if (r > kMaxN) return QR_EUNSUPPORTED;
+  return to_status(
+      run_trail(H, sHb, ldh, j0, nblk, r, c, T, sTb, batch, static_cast<hipStream_t>(stream)));
 }
 
 int qr_trace_enable(unsigned kernel_mask) {

@@ -1,0 +1,478 @@
+// qr_blocked.hip -- kernels (b) panel and (d) trailing update of the blocked
+// factorisation, both built on one register layout and one MFMA routine.
+//
+// Reference: the right-looking blocked loop of src/qrbench/variants.py:786-805,
+// the fused panel kernel _hh_panel_kernel (src/qrbench/triton_kernels.py:787-909)
+// and the trailing GEMMs C -= V (T^T (V^T C)) at variants.py:800-804.
+//
+// Two-level blocking. The matrix is processed in outer blocks of P 16-wide
+// panels (NB = 16 P columns). Inside an outer block, panel p is factored by
+// k_panel, which first applies panels 0..p-1 of the same outer block to its 16
+// columns (left-looking, so no extra launches), then factors them and writes
+// V_p (in place), tau_p and the 16 x 16 compact-WY factor T_p. The columns right
+// of the outer block are then updated by k_trail: each workgroup holds a 16-wide
+// strip of C (all r rows) in VGPRs and applies the P block reflectors one after
+// the other, so C crosses HBM once per outer block instead of once per panel.
+//
+// Strip layout (shared by both kernels): NW waves, lane l owns column l & 15;
+// VGPR m = 4t + v holds row 16 (t NW + w) + 4 (l >> 4) + v. For a 16-row tile
+// this is exactly the accumulator layout of v_mfma_f32_16x16x4_f32
+// (D[4 (l/16) + v][l % 16]), and with the K order {v, v+4, v+8, v+12} it is also
+// the B-operand layout, so W = V^T C and C -= V W2 run on MFMA straight from the
+// registers that hold C.
+#include "qr_device.hpp"
+
+namespace qr {
+
+template <int NW, int RL>
+struct Strip {
+  static_assert(RL % 4 == 0, "RL must be a multiple of 4");
+  static constexpr int kTiles = RL / 4;
+  static constexpr int kRows = 4 * NW * RL;
+  __device__ static __forceinline__ int row(int t, int v, int w, int g) {
+    return 16 * (t * NW + w) + 4 * g + v;
+  }
+  __device__ static __forceinline__ int tile_row0(int t, int w) { return 16 * (t * NW + w); }
+};
+
+// LDS of apply_wy16: each wave stages its own rows of V_q (up to kStageTiles
+// 16-row tiles at a time, row stride 20 floats: conflict-free for both the
+// b32 reads of the W phase and the b128 reads of the update phase), plus the
+// cross-wave reduction of W and the 16 x 16 T and W2.
+constexpr int kVStride = 20;
+
+// 16-row tiles of V staged per wave at a time (LDS budget: NW * tiles * 1.25 KB).
+template <int NW, int RL>
+struct StageTiles {
+  static constexpr int kMax = NW >= 16 ? 4 : 8;
+  static constexpr int value = (RL / 4) < kMax ? (RL / 4) : kMax;
+};
+
+template <int NW, int RL>
+struct WyShared {
+  float vbuf[NW][StageTiles<NW, RL>::value * 16 * kVStride];
+  float red[NW][16][17];
+  float wsum[16][17];
+  float w2[16][17];
+  float ts[16][17];
+};
+
+// Element (i, col) of the unit lower-trapezoidal block V stored in place at P
+// with rows 0..rv-1; i may be negative (rows above the block are zero).
+__device__ __forceinline__ float v_elem(const float* __restrict__ P, int64_t ldh, int i, int col,
+                                        int rv) {
+  if (i < col || i >= rv) return 0.0f;
+  if (i == col) return 1.0f;
+  return P[(int64_t)i * ldh + col];
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stage this wave's tiles [t0, t0 + kStageTiles) of V_q into vb (tile-local
+// index tt = t - t0): lane l copies row l/4, columns 4(l%4)..+3 of each tile.
+// Rows above V_q's diagonal are zero, the diagonal is 1, rows >= r are zero.
+template <int NW, int RL>
+__device__ __forceinline__ void stage_v(float* __restrict__ vb, const float* __restrict__ Vq,
+                                        int64_t ldh, int q16, int r, int t0, int w, int lane,
+                                        bool vec4) {
+  constexpr int kStageTiles = StageTiles<NW, RL>::value;
+  const int lr = lane >> 2, lc = 4 * (lane & 3);
+#pragma unroll
+  for (int tt = 0; tt < kStageTiles; ++tt) {
+    const int t = t0 + tt;
+    if (t >= RL / 4) break;
+    const int r0 = 16 * (t * NW + w);
+    if (r0 + 16 <= q16 || r0 >= r) continue;
+    const int i = r0 + lr - q16;  // row within V_q
+    f32x4 val = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (i >= 0 && r0 + lr < r) {
+      const float* src = Vq + (int64_t)i * ldh + lc;
+      if (vec4) {
+        val = *reinterpret_cast<const f32x4*>(src);
+      } else {
+        val[0] = src[0];
+        val[1] = src[1];
+        val[2] = src[2];
+        val[3] = src[3];
+      }
+      if (i < 16) {  // diagonal tile: unit lower-triangular mask
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = (lc + e > i) ? 0.0f : ((lc + e == i) ? 1.0f : val[e]);
+      }
+    }
+    *reinterpret_cast<f32x4*>(&vb[(tt * 16 + lr) * kVStride + lc]) = val;
+  }
+}
+
+// c (a 16-column strip of r rows, strip layout) := (I - V T V^T)^T c for the
+// 16-wide reflector block V stored at Vq (its row 0 is strip row q16), T = Tq.
+// Three workgroup barriers; every thread of the workgroup must call it.
+template <int NW, int RL>
+__device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restrict__ Vq,
+                                           int64_t ldh, int q16, int r,
+                                           const float* __restrict__ Tq, WyShared<NW, RL>& sh,
+                                           int w, int lane) {
+  using S = Strip<NW, RL>;
+  constexpr int kStageTiles = StageTiles<NW, RL>::value;
+  constexpr int kChunks = (S::kTiles + kStageTiles - 1) / kStageTiles;
+  const int ii = lane & 15, kk = lane >> 4;
+  const bool vec4 = ((ldh & 3) == 0) && ((reinterpret_cast<uintptr_t>(Vq) & 15) == 0);
+  float* vb = sh.vbuf[w];
+  if (threadIdx.x < 256) sh.ts[threadIdx.x >> 4][threadIdx.x & 15] = Tq[threadIdx.x];
+
+  // W (16 x 16) = V^T c, partial over this wave's rows.
+  f32x4 accw = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4);
+    wave_sync();
+#pragma unroll
+    for (int tt = 0; tt < kStageTiles; ++tt) {
+      const int t = ch * kStageTiles + tt;
+      if (t >= S::kTiles) break;
+      const int r0 = S::tile_row0(t, w);
+      if (r0 + 16 <= q16 || r0 >= r) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float av = vb[(tt * 16 + 4 * kk + v) * kVStride + ii];
+        accw = __builtin_amdgcn_mfma_f32_16x16x4f32(av, c[4 * t + v], accw, 0, 0, 0);
+      }
+    }
+    if (kChunks > 1) wave_sync();
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sh.red[w][4 * kk + v][ii] = accw[v];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) s += sh.red[u][i][j];
+    sh.wsum[i][j] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    // W2 = T^T W  (T upper triangular)
+    const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (q <= i) s = fmaf(sh.ts[q][i], sh.wsum[q][j], s);
+    sh.w2[i][j] = s;
+  }
+  __syncthreads();
+
+  // c -= V W2, with the K (reflector) order permuted so that lane (ii, kk)
+  // reads V[row ii][4kk .. 4kk+3] as one b128 and W2[4kk + s][ii].
+  float bw[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) bw[s] = sh.w2[4 * kk + s][ii];
+#pragma unroll
+  for (int ch = kChunks - 1; ch >= 0; --ch) {
+    if (ch != kChunks - 1) {
+      wave_sync();
+      stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4);
+      wave_sync();
+    }
+#pragma unroll
+    for (int tt = 0; tt < kStageTiles; ++tt) {
+      const int t = ch * kStageTiles + tt;
+      if (t >= S::kTiles) break;
+      const int r0 = S::tile_row0(t, w);
+      if (r0 + 16 <= q16 || r0 >= r) continue;
+      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&vb[(tt * 16 + ii) * kVStride + 4 * kk]);
+      f32x4 acc = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-a4[s], bw[s], acc, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) c[4 * t + v] = acc[v];
+    }
+  }
+  __syncthreads();  // sh is reused by the next call
+}
+
+template <int NW, int RL>
+__device__ __forceinline__ void load_strip(float (&c)[RL], const float* __restrict__ P,
+                                           int64_t ldh, int r, int ncol, int w, int lane) {
+  using S = Strip<NW, RL>;
+  const int k = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < S::kTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = S::row(t, v, w, g);
+      c[4 * t + v] = (row < r && k < ncol) ? P[(int64_t)row * ldh + k] : 0.0f;
+    }
+}
+
+// Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
+// Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
+// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p.
+template <int NW, int RL>
+__global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
+                                                   int64_t ldh, int J0, int p, int r, int kw,
+                                                   float* __restrict__ tau, int64_t sTaub,
+                                                   float* __restrict__ Tws, int64_t sTwb) {
+  using S = Strip<NW, RL>;
+  __shared__ WyShared<NW, RL> wy;
+  __shared__ __align__(16) float xs[NW][4 * RL];
+  __shared__ float red[2][NW][16];
+  __shared__ float erow[2][16];
+  __shared__ float zbuf[16][17];
+  __shared__ float tbuf[16][17];
+  __shared__ float taus[16];
+  __shared__ float scr[2][NW];
+
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int k = lane & 15, g = lane >> 4;
+  float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
+  float* P = Blk + 16 * p;
+  float* Tb = Tws + (int64_t)b * sTwb;
+
+  float c[RL];
+  load_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
+  for (int q = 0; q < p; ++q)
+    apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q, wy,
+                       w, lane);
+
+  // The diagonal rows 16p..16p+15 are tile 0 of wave p (NW > p is required).
+  const int d0 = 16 * p;
+  float my_beta = 0.0f, my_gamma = 1.0f, my_pre = 1.0f, my_tau = 0.0f;
+  float* xw = xs[w];
+
+  for (int j = 0; j < kw; ++j) {
+    const int dj = d0 + j;
+    __builtin_amdgcn_wave_barrier();
+    // Lanes of column j publish x = column j below the diagonal (this wave's rows).
+    if (k == j) {
+#pragma unroll
+      for (int t = 0; t < S::kTiles; ++t) {
+        f32x4 xv;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xv[v] = (S::row(t, v, w, g) > dj) ? c[4 * t + v] : 0.0f;
+        *reinterpret_cast<f32x4*>(&xw[16 * t + 4 * g]) = xv;
+      }
+    }
+    if (w == p && g == (j >> 2)) {
+      const int v = j & 3;
+      erow[j & 1][k] = (v == 0) ? c[0] : (v == 1) ? c[1] : (v == 2) ? c[2] : c[3];
+    }
+    wave_sync();
+    float d = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S::kTiles; ++t) {
+      if (S::tile_row0(t, w) >= r) continue;
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xw[16 * t + 4 * g]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) d = fmaf(xv[v], c[4 * t + v], d);
+    }
+    d = sum_over_rows16(d);
+    if (g == 0) red[j & 1][w][k] = d;
+    __syncthreads();
+    float ds = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) ds += red[j & 1][u][k];
+    const float e = erow[j & 1][k];
+    const float sigma = readlane_f(ds, j);
+    const float alpha = readlane_f(e, j);
+
+    Reflector R;
+    bool fast = true;
+    if (dj >= r - 1) {
+      R = reflector_identity(alpha);
+    } else if (reflector_fast_ok(alpha, sigma)) {
+      R = reflector_fast(alpha, sigma);
+    } else {
+      // Scaled norm of x from the per-wave slabs: two workgroup reductions.
+      float xm = 0.0f;
+      for (int idx = lane; idx < 4 * RL; idx += 64) xm = fmaxf(xm, fabsf(xw[idx]));
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) xm = fmaxf(xm, __shfl_xor(xm, o));
+      if (lane == 0) scr[0][w] = xm;
+      __syncthreads();
+      float xmax = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NW; ++u) xmax = fmaxf(xmax, scr[0][u]);
+      float s = 0.0f;
+      if (xmax > 0.0f) {
+        for (int idx = lane; idx < 4 * RL; idx += 64) {
+          const float tq = xw[idx] / xmax;
+          s = fmaf(tq, tq, s);
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+      if (lane == 0) scr[1][w] = s;
+      __syncthreads();
+      float ssq = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NW; ++u) ssq += scr[1][u];
+      R = reflector_scaled(alpha, xmax, ssq);
+      fast = false;
+    }
+
+    const bool upd = (k > j) && (k < kw);
+    const bool own_row = (w == p) && (g == (j >> 2));
+    if (fast || R.tau != 0.0f) {
+      const float wk = fast ? fmaf(R.gamma, ds, e) : fmaf(R.gamma, R.pre * ds, e);
+      const float cc = R.tau * wk;
+      // fast: c -= (cc gamma) x;  slow: c -= cc ((x pre) gamma)
+      const float cx = upd ? (fast ? cc * R.gamma : cc) : 0.0f;
+#pragma unroll
+      for (int t = 0; t < S::kTiles; ++t) {
+        if (S::tile_row0(t, w) >= r) continue;
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(&xw[16 * t + 4 * g]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float xe = fast ? xv[v] : (xv[v] * R.pre) * R.gamma;
+          c[4 * t + v] = fmaf(-cx, xe, c[4 * t + v]);
+        }
+      }
+      if (upd && own_row) {
+        const int v = j & 3;
+        if (v == 0) c[0] -= cc;
+        else if (v == 1) c[1] -= cc;
+        else if (v == 2) c[2] -= cc;
+        else c[3] -= cc;
+      }
+    }
+    // Column j of T needs z_k = V_k^T v_j for k < j.
+    if (w == 0 && g == 0 && k < j)
+      zbuf[j][k] = (my_pre * my_gamma) * fmaf(R.pre * R.gamma, ds, e);
+    if (k == j) {
+      my_beta = R.beta;
+      my_gamma = R.gamma;
+      my_pre = R.pre;
+      my_tau = R.tau;
+    }
+  }
+  if (w == 0 && g == 0) taus[k] = (k < kw) ? my_tau : 0.0f;
+  __syncthreads();
+
+  // T_p (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
+  if (w == 0 && g == 0) {
+    for (int j = 0; j < 16; ++j) {
+      float val = 0.0f;
+      if (j < kw) {
+        const float tj = taus[j];
+        if (k < j) {
+          float s = 0.0f;
+          for (int q = k; q < j; ++q) s = fmaf(tbuf[k][q], zbuf[j][q], s);
+          val = -tj * s;
+        } else if (k == j) {
+          val = tj;
+        }
+      }
+      tbuf[k][j] = val;
+      wave_sync();
+    }
+    float* Tp = Tb + 256 * p;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) Tp[k * 16 + q] = tbuf[k][q];
+    if (k < kw) tau[(int64_t)b * sTaub + J0 + d0 + k] = my_tau;
+  }
+
+  // Write back: R above the diagonal, beta on it, v = (x pre) gamma below.
+  const int kd = d0 + k;
+#pragma unroll
+  for (int t = 0; t < S::kTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = S::row(t, v, w, g);
+      if (row < r && k < kw) {
+        const float val =
+            (row < kd) ? c[4 * t + v] : ((row == kd) ? my_beta : (c[4 * t + v] * my_pre) * my_gamma);
+        P[(int64_t)row * ldh + k] = val;
+      }
+    }
+}
+
+// Columns c0.. c0+ncols-1 (relative to the outer block at J0, r rows) :=
+// Q^T C with the nblk 16-wide reflector blocks of the outer block, applied
+// in order 0..nblk-1. Grid (ceil(ncols / 16), batch); one strip per workgroup.
+template <int NW, int RL>
+__global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_t sHb,
+                                                   int64_t ldh, int J0, int nblk, int r, int c0,
+                                                   int ncols, const float* __restrict__ Tws,
+                                                   int64_t sTwb) {
+  __shared__ WyShared<NW, RL> wy;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
+  const int s0 = 16 * blockIdx.x;
+  float* P = Blk + c0 + s0;
+  const float* Tb = Tws + (int64_t)b * sTwb;
+  const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
+
+  float c[RL];
+  load_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
+  for (int q = 0; q < nblk; ++q)
+    apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q, wy,
+                       w, lane);
+  using S = Strip<NW, RL>;
+  const int k = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < S::kTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = S::row(t, v, w, g);
+      if (row < r && k < ncol) P[(int64_t)row * ldh + k] = c[4 * t + v];
+    }
+}
+
+// (NW, RL) for r rows: 4 NW RL >= r and NW > p for every panel index used.
+#define QR_STRIP_DISPATCH(r, CASE)   \
+  if ((r) <= 128) {                  \
+    CASE(8, 4);                      \
+  } else if ((r) <= 256) {           \
+    CASE(8, 8);                      \
+  } else if ((r) <= 512) {           \
+    CASE(8, 16);                     \
+  } else if ((r) <= 1024) {          \
+    CASE(8, 32);                     \
+  } else if ((r) <= 2048) {          \
+    CASE(8, 64);                     \
+  } else {                           \
+    CASE(16, 64);                    \
+  }
+
+constexpr int kMaxStripRows = 4096;
+constexpr int kMaxBlocks = 8;
+
+hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
+                        float* tau, int64_t sTaub, float* Tws, int64_t sTwb, int batch,
+                        hipStream_t stream) {
+  if (kw < 1 || kw > 16 || p < 0 || p >= kMaxBlocks || r > kMaxStripRows || r < 16 * p + kw)
+    return hipErrorInvalidValue;
+#define QR_PANEL_CASE(NWV, RLV)                                                             \
+  hipLaunchKernelGGL((k_panel<NWV, RLV>), dim3(batch), dim3(64 * NWV), 0, stream, H, sHb, ldh, \
+                     J0, p, r, kw, tau, sTaub, Tws, sTwb)
+  QR_STRIP_DISPATCH(r, QR_PANEL_CASE)
+#undef QR_PANEL_CASE
+  return hipGetLastError();
+}
+
+hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
+                        int ncols, const float* Tws, int64_t sTwb, int batch,
+                        hipStream_t stream) {
+  if (ncols <= 0) return hipSuccess;
+  if (nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || r < 16 * (nblk - 1) + 1)
+    return hipErrorInvalidValue;
+  const dim3 grid((ncols + 15) / 16, batch);
+#define QR_TRAIL_CASE(NWV, RLV)                                                              \
+  hipLaunchKernelGGL((k_trail<NWV, RLV>), grid, dim3(64 * NWV), 0, stream, H, sHb, ldh, J0, \
+                     nblk, r, c0, ncols, Tws, sTwb)
+  QR_STRIP_DISPATCH(r, QR_TRAIL_CASE)
+#undef QR_TRAIL_CASE
+  return hipGetLastError();
+}
+
+}  // namespace qr

@@ -82,28 +82,34 @@ def fused_smalln(A: torch.Tensor):
     return H, tau
 
 
-def panel(P: torch.Tensor):
-    """Kernel (b) alone on a batch of (r, kw) panels (kw <= 16).
+def panel(P: torch.Tensor, p: int = 0, T_prev: torch.Tensor | None = None):
+    """Kernel (b) alone on a batch of (r, 16 p + kw) blocks (kw <= 16).
 
-    Returns ``(H_p, tau, T)``: the factored panel in geqrf packing, its ``kw``
-    reflector coefficients and the 16 x 16 compact-WY factor (upper, zero
-    beyond ``kw``), like the reference's ``hh_panel_qr`` minus the explicit V
+    Panels 0..p-1 of each block must already be factored in place (V below the
+    diagonal) with their 16 x 16 T factors in ``T_prev`` (batch, p, 16, 16).
+    Panel p (columns 16p..16p+kw-1) first gets Q_{0..p-1}^T applied, then is
+    factored. Returns ``(H_blk, tau_p, T_p)``: the block with panel p factored in
+    geqrf packing, its kw reflector coefficients and its 16 x 16 T (zero beyond
+    kw), like the reference's ``hh_panel_qr`` minus the explicit V
     (src/qrbench/triton_kernels.py:912-967).
     """
     if P.dim() != 3 or P.dtype != torch.float32 or P.device.type != "cuda":
-        raise ValueError("P must be a (batch, r, kw) float32 GPU tensor")
+        raise ValueError("P must be a (batch, r, width) float32 GPU tensor")
     lib = _lib.load()
-    b, r, kw = P.shape
+    b, r, width = P.shape
+    kw = width - PANEL * p
     Hp = P.contiguous().clone()
-    tau = torch.zeros((b, kw), dtype=torch.float32, device=P.device)
-    T = torch.empty((b, PANEL, PANEL), dtype=torch.float32, device=P.device)
+    tau = torch.zeros((b, width), dtype=torch.float32, device=P.device)
+    T = torch.zeros((b, p + 1, PANEL, PANEL), dtype=torch.float32, device=P.device)
+    if p:
+        T[:, :p] = T_prev
     with torch.cuda.device(P.device):
         st = lib.qr_panel_f32(
-            Hp.data_ptr(), r * kw, kw, 0, r, kw, tau.data_ptr(), kw, T.data_ptr(), PANEL * PANEL,
-            b, _stream(P.device),
+            Hp.data_ptr(), r * width, width, 0, p, r, kw, tau.data_ptr(), width, T.data_ptr(),
+            (p + 1) * PANEL * PANEL, b, _stream(P.device),
         )
     _lib.check("qr_panel_f32", st)
-    return Hp, tau, T
+    return Hp, tau[:, PANEL * p:], T[:, p]
 
 
 def larft(V: torch.Tensor, tau: torch.Tensor):
@@ -124,20 +130,21 @@ def larft(V: torch.Tensor, tau: torch.Tensor):
     return T
 
 
-def wy_update(Hpanel: torch.Tensor, T: torch.Tensor):
-    """Kernel (d) alone: given a (batch, r, 16 + c) block whose first 16 columns
-    hold a factored panel (V below the diagonal) and T (batch, 16, 16), return a
-    copy with the last c columns replaced by C - V T^T V^T C."""
+def wy_update(Hblk: torch.Tensor, T: torch.Tensor):
+    """Kernel (d) alone: ``Hblk`` (batch, r, 16 nblk + c) holds nblk factored
+    16-wide panels (V below the diagonal) followed by c columns C; ``T``
+    (batch, nblk, 16, 16) their T factors. Returns a copy with C replaced by
+    Q^T C = (H_{nblk-1} ... H_0) C."""
     lib = _lib.load()
-    b, r, width = Hpanel.shape
-    c = width - PANEL
-    out = Hpanel.contiguous().clone()
+    b, r, width = Hblk.shape
+    nblk = T.shape[1]
+    c = width - PANEL * nblk
+    out = Hblk.contiguous().clone()
     Tc = T.contiguous()
-    ws = torch.empty(max(1, b * PANEL * c * 4), dtype=torch.uint8, device=Hpanel.device)
-    with torch.cuda.device(Hpanel.device):
+    with torch.cuda.device(Hblk.device):
         st = lib.qr_wy_update_f32(
-            out.data_ptr(), r * width, width, 0, r, c, Tc.data_ptr(), PANEL * PANEL,
-            ws.data_ptr(), ws.numel(), b, _stream(Hpanel.device),
+            out.data_ptr(), r * width, width, 0, nblk, r, c, Tc.data_ptr(),
+            nblk * PANEL * PANEL, b, _stream(Hblk.device),
         )
     _lib.check("qr_wy_update_f32", st)
     return out

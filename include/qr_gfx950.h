@@ -33,12 +33,11 @@ typedef enum qr_status {
 
 /* Kernel identifiers for the launch tracer (bit i of the trace mask). */
 typedef enum qr_kernel_id {
-  QR_KERNEL_SMALLN = 0,   /* kernel (a) */
-  QR_KERNEL_PANEL = 1,    /* kernel (b) */
-  QR_KERNEL_WY_W2 = 2,    /* kernel (d), W2 = T^T V^T C */
-  QR_KERNEL_WY_APPLY = 3, /* kernel (d), C -= V W2 */
-  QR_KERNEL_COPY = 4,     /* strided A -> H copy */
-  QR_KERNEL_LARFT = 5     /* kernel (c) */
+  QR_KERNEL_SMALLN = 0, /* kernel (a) */
+  QR_KERNEL_PANEL = 1,  /* kernel (b), incl. its left-looking block update */
+  QR_KERNEL_TRAIL = 2,  /* kernel (d), trailing compact-WY update */
+  QR_KERNEL_COPY = 3,   /* strided A -> H copy */
+  QR_KERNEL_LARFT = 4   /* kernel (c) */
 } qr_kernel_id;
 
 /* Human-readable text for a qr_status value (static storage). */
@@ -74,13 +73,18 @@ int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, f
                         float* tau, int batch, int n, void* stream);
 
 /*
- * Kernel (b): in-place factorisation of the r x kw panel (kw <= 16, r >= kw)
- * whose top-left element is H[b*sHb + j0*ldh + j0], writing tau[b*sTaub + j0 + i]
- * and the panel's 16 x 16 upper T (row-major, zero beyond kw) to T[b*sTb ...].
+ * Kernel (b): factor panel p (0 <= p < 8, width kw <= 16) of the outer block
+ * whose top-left element is H[b*sHb + j0*ldh + j0] and which has r rows.
+ * The panel's columns are j0+16p .. j0+16p+kw-1 and its diagonal starts at row
+ * j0+16p. Panels 0..p-1 of the same block must already be factored, with their
+ * 16 x 16 upper T factors at T[b*sTb + 256q]; they are applied to the panel's
+ * columns first (left-looking). Writes V / R in place, tau[b*sTaub + j0+16p+i]
+ * and the panel's T (zero beyond kw) at T[b*sTb + 256p].
  * Replaces hh_panel_qr / _hh_panel_kernel (reference
- * src/qrbench/triton_kernels.py:787-967), which returns (H_p, V, tau, T).
+ * src/qrbench/triton_kernels.py:787-967), which returns (H_p, V, tau, T), and
+ * the in-block part of the trailing GEMMs (src/qrbench/variants.py:800-804).
  */
-int qr_panel_f32(float* H, int64_t sHb, int64_t ldh, int j0, int r, int kw, float* tau,
+int qr_panel_f32(float* H, int64_t sHb, int64_t ldh, int j0, int p, int r, int kw, float* tau,
                  int64_t sTaub, float* T, int64_t sTb, int batch, void* stream);
 
 /*
@@ -92,14 +96,14 @@ int qr_larft_f32(const float* V, int64_t sVb, int64_t ldv, int m, int k, const f
                  int64_t sTaub, float* T, int64_t sTb, int64_t ldt, int batch, void* stream);
 
 /*
- * Kernel (d): C -= V T^T V^T C for the 16-wide reflector block of the panel at
- * (j0, j0) and the c columns right of it (C = H[.. j0 .., j0+16 : j0+16+c]),
- * r rows. T as written by qr_panel_f32. Workspace: 16 * c floats per matrix.
+ * Kernel (d): C := Q^T C for the nblk <= 8 factored 16-wide panels of the outer
+ * block at (j0, j0) (r rows; their T factors at T[b*sTb + 256q]), where C is
+ * the c columns starting at column j0 + 16*nblk, rows j0 .. j0+r-1. The blocks
+ * are applied in order 0..nblk-1, each as C -= V_q T_q^T V_q^T C.
  * Replaces the trailing GEMMs of reference src/qrbench/variants.py:800-804.
  */
-int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int r, int c, const float* T,
-                     int64_t sTb, void* workspace, size_t workspace_bytes, int batch,
-                     void* stream);
+int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int nblk, int r, int c,
+                     const float* T, int64_t sTb, int batch, void* stream);
 
 /*
  * Launch tracer (measurement only; no counterpart in the reference, whose

@@ -61,11 +61,29 @@ def test_fused_smalln_strided_input(oracle):
     assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref)
 
 
+def _oracle_panels(oracle, blk, nfact):
+    """Oracle blocked factorisation of the first nfact 16-wide panels of blk
+    (r, width): returns (H, taus, Ts) with the trailing columns updated."""
+    H = blk.copy()
+    r = H.shape[0]
+    taus, Ts = [], []
+    for q in range(nfact):
+        c0 = 16 * q
+        Hq, tq = oracle.geqr2(H[c0:, c0:c0 + 16])
+        H[c0:, c0:c0 + 16] = Hq
+        Tq = oracle.larft(Hq, tq)
+        if H.shape[1] > c0 + 16:
+            H[c0:, c0 + 16:] = oracle.larfb_lt(Hq, Tq, H[c0:, c0 + 16:])
+        taus.append(tq)
+        Ts.append(Tq)
+    return H, taus, Ts
+
+
 @pytest.mark.parametrize("r,kw", [(16, 16), (17, 16), (40, 16), (64, 16), (100, 16), (256, 16),
                                   (300, 16), (777, 16), (1024, 16), (2048, 16), (2049, 16),
                                   (3000, 16), (64, 5), (20, 13)])
 def test_panel_vs_oracle(oracle, r, kw):
-    _say(f"panel r={r} kw={kw}")
+    _say(f"panel p=0 r={r} kw={kw}")
     g = torch.Generator().manual_seed(r * 31 + kw)
     P = torch.randn(3, r, kw, generator=g)
     Hp, tau, T = hip_qr.panel(P.to(DEV))
@@ -83,6 +101,33 @@ def test_panel_vs_oracle(oracle, r, kw):
         assert np.abs(tau[b] - tr).max() <= tol, "tau"
         assert np.abs(T[b, :kw, :kw] - Tr).max() <= 4 * tol, "T"
         assert np.all(T[b, kw:, :] == 0) and np.all(T[b, :, kw:] == 0)
+
+
+@pytest.mark.parametrize("r,p,kw", [(48, 1, 16), (100, 2, 16), (300, 3, 16), (512, 7, 16),
+                                    (2048, 3, 16), (90, 5, 10), (3000, 2, 16)])
+def test_panel_left_looking_vs_oracle(oracle, r, p, kw):
+    _say(f"panel left-looking r={r} p={p} kw={kw}")
+    g = torch.Generator().manual_seed(r + 7 * p + kw)
+    blk = torch.randn(2, r, 16 * p + kw, generator=g).numpy()
+    for b in range(2):
+        # panels 0..p-1 factored by the oracle; panel p still raw
+        Hpre, _, Ts = _oracle_panels(oracle, np.concatenate(
+            [blk[b][:, :16 * p], np.zeros((r, 0), np.float32)], axis=1), p)
+        start = np.concatenate([Hpre, blk[b][:, 16 * p:]], axis=1)
+        T_prev = torch.from_numpy(np.stack(Ts)[None]).to(DEV)
+        Hg, tau, T = hip_qr.panel(torch.from_numpy(start[None]).to(DEV), p=p, T_prev=T_prev)
+        torch.cuda.synchronize()
+        Hg, tau, T = Hg.cpu().numpy()[0], tau.cpu().numpy()[0], T.cpu().numpy()[0]
+        Href, taus, Trefs = _oracle_panels(oracle, blk[b], p + 1)
+        assert np.array_equal(Hg[:, :16 * p], start[:, :16 * p])  # earlier panels untouched
+        tol = 4 * r * 2**-23
+        colnorm = np.linalg.norm(blk[b][:, 16 * p:].astype(np.float64), axis=0)
+        up = np.triu(np.ones((r, kw), bool), k=-16 * p)
+        dH = np.abs(Hg[:, 16 * p:].astype(np.float64) - Href[:, 16 * p:])
+        assert (np.where(up, dH / colnorm, 0)).max() <= tol, "R"
+        assert (np.where(~up, dH, 0)).max() <= tol, "V"
+        assert np.abs(tau - taus[p]).max() <= tol, "tau"
+        assert np.abs(T[:kw, :kw] - Trefs[p]).max() <= 4 * tol, "T"
 
 
 @pytest.mark.parametrize("m,k", [(16, 16), (64, 16), (300, 32), (1000, 64), (40, 7)])
@@ -105,33 +150,29 @@ def test_larft_vs_oracle(oracle, m, k):
         assert np.abs(T[b] - Trefs[b]).max() <= 16 * m * 2**-23
 
 
-@pytest.mark.parametrize("r,c", [(16, 1), (64, 48), (100, 77), (512, 496), (1030, 200)])
-def test_wy_update_vs_oracle(oracle, r, c):
-    _say(f"wy_update r={r} c={c}")
-    g = torch.Generator().manual_seed(r + 3 * c)
-    P = torch.randn(2, r, 16, generator=g)
-    C = torch.randn(2, r, c, generator=g)
-    blocks, Ts, refs = [], [], []
+@pytest.mark.parametrize("r,nblk,c", [(16, 1, 1), (64, 1, 48), (100, 2, 77), (512, 4, 448),
+                                      (1030, 3, 200), (2048, 4, 40), (300, 8, 33), (2500, 2, 20)])
+def test_wy_update_vs_oracle(oracle, r, nblk, c):
+    _say(f"wy_update r={r} nblk={nblk} c={c}")
+    g = torch.Generator().manual_seed(r + 3 * c + nblk)
+    blk = torch.randn(2, r, 16 * nblk + c, generator=g).numpy()
+    starts, Ts, refs = [], [], []
     for b in range(2):
-        Hr, tr = oracle.geqr2(P[b].numpy())
-        Tr = oracle.larft(Hr, tr)
-        T16 = np.zeros((16, 16), np.float32)
-        T16[:16, :16] = Tr
-        Ts.append(T16)
-        blocks.append(np.concatenate([Hr, C[b].numpy()], axis=1))
-        refs.append(oracle.larfb_lt(Hr, Tr, C[b].numpy()))
-    blk = torch.from_numpy(np.stack(blocks)).to(DEV)
-    T = torch.from_numpy(np.stack(Ts)).to(DEV)
-    out = hip_qr.wy_update(blk, T)
+        Hp, _, Tb = _oracle_panels(oracle, blk[b][:, :16 * nblk], nblk)
+        starts.append(np.concatenate([Hp, blk[b][:, 16 * nblk:]], axis=1))
+        Ts.append(np.stack(Tb))
+        refs.append(_oracle_panels(oracle, blk[b], nblk)[0][:, 16 * nblk:])
+    out = hip_qr.wy_update(torch.from_numpy(np.stack(starts)).to(DEV),
+                           torch.from_numpy(np.stack(Ts)).to(DEV))
     torch.cuda.synchronize()
     out = out.cpu().numpy()
     for b in range(2):
-        assert np.array_equal(out[b, :, :16], blocks[b][:, :16])  # V untouched
-        scale = max(1.0, float(np.abs(C[b].numpy()).max()))
-        assert np.abs(out[b, :, 16:] - refs[b]).max() <= 16 * r * 2**-23 * scale
+        assert np.array_equal(out[b, :, :16 * nblk], starts[b][:, :16 * nblk])  # V untouched
+        scale = max(1.0, float(np.abs(blk[b]).max()))
+        assert np.abs(out[b, :, 16 * nblk:] - refs[b]).max() <= 16 * r * 2**-23 * scale
 
 
-@pytest.mark.parametrize("n", [65, 80, 96, 128, 129, 176, 200, 352, 512])
+@pytest.mark.parametrize("n", [65, 80, 96, 128, 129, 176, 200, 352, 512, 700, 1100])
 def test_geqrf_blocked_vs_oracle(oracle, n):
     _say(f"geqrf blocked n={n}")
     A = _gauss(3, n, seed=n)

@@ -57,7 +57,7 @@ def test_workspace_query(lib):
     assert lib.qr_geqrf_f32_workspace(64, 32) == 0  # fused route needs none
     assert lib.qr_geqrf_f32_workspace(0, 512) == 0
     ws = lib.qr_geqrf_f32_workspace(640, 512)
-    assert ws >= 640 * (16 * 16 + 16 * 512) * 4
+    assert ws >= 640 * 8 * 16 * 16 * 4
     assert ws % 256 == 0
 
 
@@ -79,6 +79,9 @@ def test_argument_validation_without_launch(lib):
     assert lib.qr_geqrf_f32(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, None) == 3
     # kernel-level entry points
     assert lib.qr_fused_smalln_f32(p, 100 * 100, 100, 1, h, t, 1, 100, None) == 2
-    assert lib.qr_panel_f32(h, 100, 10, 0, 10, 17, t, 17, t, 256, 1, None) == 1
+    assert lib.qr_panel_f32(h, 100, 10, 0, 0, 10, 17, t, 17, t, 256, 1, None) == 1  # kw > 16
+    assert lib.qr_panel_f32(h, 9000, 90, 0, 8, 200, 16, t, 90, t, 4096, 1, None) == 1  # p >= 8
+    assert lib.qr_panel_f32(h, 9000, 90, 0, 2, 40, 16, t, 90, t, 512, 1, None) == 1  # r < 16p+kw
     assert lib.qr_larft_f32(h, 100, 70, 100, 70, t, 70, t, 4900, 70, 1, None) == 2
-    assert lib.qr_wy_update_f32(h, 1000, 50, 0, 20, 34, t, 256, None, 0, 1, None) == 3
+    assert lib.qr_wy_update_f32(h, 1000, 50, 0, 9, 200, 4, t, 4096, 1, None) == 1  # nblk > 8
+    assert lib.qr_wy_update_f32(h, 1000, 50, 0, 2, 5000, 4, t, 512, 1, None) == 2  # r > 4096
