@@ -201,13 +201,41 @@ __device__ __forceinline__ void load_strip(float (&c)[RL], const float* __restri
                                            int64_t ldh, int r, int ncol, int w, int lane) {
   using S = Strip<NW, RL>;
   const int k = lane & 15, g = lane >> 4;
+  const bool colok = k < ncol;
+  const float* src = P + (int64_t)(16 * w + 4 * g) * ldh + k;
+  const int64_t tstep = (int64_t)16 * NW * ldh;
 #pragma unroll
-  for (int t = 0; t < S::kTiles; ++t)
+  for (int t = 0; t < S::kTiles; ++t) {
+    const int r0 = S::tile_row0(t, w);
+    if (r0 + 16 <= r) {  // whole tile inside (uniform)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = S::row(t, v, w, g);
-      c[4 * t + v] = (row < r && k < ncol) ? P[(int64_t)row * ldh + k] : 0.0f;
+      for (int v = 0; v < 4; ++v) c[4 * t + v] = colok ? src[v * ldh] : 0.0f;
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        c[4 * t + v] = (colok && r0 + 4 * g + v < r) ? src[v * ldh] : 0.0f;
     }
+    src += tstep;
+  }
+}
+
+template <int NW, int RL>
+__device__ __forceinline__ void store_strip(const float (&c)[RL], float* __restrict__ P,
+                                            int64_t ldh, int r, int ncol, int w, int lane) {
+  using S = Strip<NW, RL>;
+  const int k = lane & 15, g = lane >> 4;
+  const bool colok = k < ncol;
+  float* dst = P + (int64_t)(16 * w + 4 * g) * ldh + k;
+  const int64_t tstep = (int64_t)16 * NW * ldh;
+#pragma unroll
+  for (int t = 0; t < S::kTiles; ++t) {
+    const int r0 = S::tile_row0(t, w);
+    if (r0 >= r) break;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (colok && r0 + 4 * g + v < r) dst[v * ldh] = c[4 * t + v];
+    dst += tstep;
+  }
 }
 
 // Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
@@ -230,7 +258,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
 
   const int b = blockIdx.x;
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int k = lane & 15, g = lane >> 4;
   float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
   float* P = Blk + 16 * p;
@@ -252,12 +280,16 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
     __builtin_amdgcn_wave_barrier();
     // Lanes of column j publish x = column j below the diagonal (this wave's rows).
     if (k == j) {
+      // Rows <= dj < 16 NW all sit in tile 0, so only tile 0 is masked.
+      f32x4 xv;
 #pragma unroll
-      for (int t = 0; t < S::kTiles; ++t) {
-        f32x4 xv;
+      for (int v = 0; v < 4; ++v) xv[v] = (S::row(0, v, w, g) > dj) ? c[v] : 0.0f;
+      *reinterpret_cast<f32x4*>(&xw[4 * g]) = xv;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) xv[v] = (S::row(t, v, w, g) > dj) ? c[4 * t + v] : 0.0f;
-        *reinterpret_cast<f32x4*>(&xw[16 * t + 4 * g]) = xv;
+      for (int t = 1; t < S::kTiles; ++t) {
+        if (S::tile_row0(t, w) >= r) break;
+        const f32x4 cv = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
+        *reinterpret_cast<f32x4*>(&xw[16 * t + 4 * g]) = cv;
       }
     }
     if (w == p && g == (j >> 2)) {
@@ -291,8 +323,12 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       R = reflector_fast(alpha, sigma);
     } else {
       // Scaled norm of x from the per-wave slabs: two workgroup reductions.
+      // Only tiles holding rows < r were published this step.
+      int nvalid = 0;
+#pragma unroll
+      for (int t = 0; t < S::kTiles; ++t) nvalid += (S::tile_row0(t, w) < r) ? 16 : 0;
       float xm = 0.0f;
-      for (int idx = lane; idx < 4 * RL; idx += 64) xm = fmaxf(xm, fabsf(xw[idx]));
+      for (int idx = lane; idx < nvalid; idx += 64) xm = fmaxf(xm, fabsf(xw[idx]));
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) xm = fmaxf(xm, __shfl_xor(xm, o));
       if (lane == 0) scr[0][w] = xm;
@@ -302,7 +338,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       for (int u = 0; u < NW; ++u) xmax = fmaxf(xmax, scr[0][u]);
       float s = 0.0f;
       if (xmax > 0.0f) {
-        for (int idx = lane; idx < 4 * RL; idx += 64) {
+        for (int idx = lane; idx < nvalid; idx += 64) {
           const float tq = xw[idx] / xmax;
           s = fmaf(tq, tq, s);
         }
@@ -357,25 +393,22 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   __syncthreads();
 
   // T_p (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
+  // Lane k of wave 0 holds row k of T in registers; z_j is read as broadcasts.
   if (w == 0 && g == 0) {
+    float trow[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) trow[q] = 0.0f;
+#pragma unroll
     for (int j = 0; j < 16; ++j) {
-      float val = 0.0f;
-      if (j < kw) {
-        const float tj = taus[j];
-        if (k < j) {
-          float s = 0.0f;
-          for (int q = k; q < j; ++q) s = fmaf(tbuf[k][q], zbuf[j][q], s);
-          val = -tj * s;
-        } else if (k == j) {
-          val = tj;
-        }
-      }
-      tbuf[k][j] = val;
-      wave_sync();
+      float s = 0.0f;
+#pragma unroll
+      for (int q = 0; q < j; ++q) s = fmaf(trow[q], zbuf[j][q], s);  // trow[q] = 0 for q < k
+      const float tj = taus[j];
+      trow[j] = (j >= kw) ? 0.0f : ((k < j) ? -tj * s : ((k == j) ? tj : 0.0f));
     }
     float* Tp = Tb + 256 * p;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) Tp[k * 16 + q] = tbuf[k][q];
+    for (int q = 0; q < 16; ++q) Tp[k * 16 + q] = trow[q];
     if (k < kw) tau[(int64_t)b * sTaub + J0 + d0 + k] = my_tau;
   }
 
@@ -386,12 +419,10 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = S::row(t, v, w, g);
-      if (row < r && k < kw) {
-        const float val =
-            (row < kd) ? c[4 * t + v] : ((row == kd) ? my_beta : (c[4 * t + v] * my_pre) * my_gamma);
-        P[(int64_t)row * ldh + k] = val;
-      }
+      c[4 * t + v] =
+          (row < kd) ? c[4 * t + v] : ((row == kd) ? my_beta : (c[4 * t + v] * my_pre) * my_gamma);
     }
+  store_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
 }
 
 // Columns c0.. c0+ncols-1 (relative to the outer block at J0, r rows) :=
@@ -405,7 +436,7 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   __shared__ WyShared<NW, RL> wy;
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
   const int s0 = 16 * blockIdx.x;
   float* P = Blk + c0 + s0;
@@ -417,15 +448,7 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   for (int q = 0; q < nblk; ++q)
     apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q, wy,
                        w, lane);
-  using S = Strip<NW, RL>;
-  const int k = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int t = 0; t < S::kTiles; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = S::row(t, v, w, g);
-      if (row < r && k < ncol) P[(int64_t)row * ldh + k] = c[4 * t + v];
-    }
+  store_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
 }
 
 // (NW, RL) for r rows: 4 NW RL >= r and NW > p for every panel index used.
