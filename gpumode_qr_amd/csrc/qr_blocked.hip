@@ -84,9 +84,8 @@ __device__ __forceinline__ void stage_v(float* __restrict__ vb, const float* __r
 #pragma unroll
   for (int tt = 0; tt < kStageTiles; ++tt) {
     const int t = t0 + tt;
-    if (t >= RL / 4) break;
+    if (t >= RL / 4) break;  // compile-time
     const int r0 = 16 * (t * NW + w);
-    if (r0 + 16 <= q16 || r0 >= r) continue;
     const int i = r0 + lr - q16;  // row within V_q
     f32x4 val = {0.0f, 0.0f, 0.0f, 0.0f};
     if (i >= 0 && r0 + lr < r) {
@@ -133,9 +132,9 @@ __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restri
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
       const int t = ch * kStageTiles + tt;
-      if (t >= S::kTiles) break;
-      const int r0 = S::tile_row0(t, w);
-      if (r0 + 16 <= q16 || r0 >= r) continue;
+      if (t >= S::kTiles) break;  // compile-time
+      // Tiles outside V_q or below the strip were staged as zeros: no branch
+      // here, so the compiler can batch the LDS reads.
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float av = vb[(tt * 16 + 4 * kk + v) * kVStride + ii];
@@ -181,9 +180,7 @@ __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restri
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
       const int t = ch * kStageTiles + tt;
-      if (t >= S::kTiles) break;
-      const int r0 = S::tile_row0(t, w);
-      if (r0 + 16 <= q16 || r0 >= r) continue;
+      if (t >= S::kTiles) break;  // compile-time
       const f32x4 a4 = *reinterpret_cast<const f32x4*>(&vb[(tt * 16 + ii) * kVStride + 4 * kk]);
       f32x4 acc = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
 #pragma unroll
@@ -231,10 +228,36 @@ __device__ __forceinline__ void store_strip(const float (&c)[RL], float* __restr
   for (int t = 0; t < S::kTiles; ++t) {
     const int r0 = S::tile_row0(t, w);
     if (r0 >= r) break;
+    if (r0 + 16 <= r) {  // whole tile inside (uniform)
+      if (colok) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      if (colok && r0 + 4 * g + v < r) dst[v * ldh] = c[4 * t + v];
+        for (int v = 0; v < 4; ++v) dst[v * ldh] = c[4 * t + v];
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (colok && r0 + 4 * g + v < r) dst[v * ldh] = c[4 * t + v];
+    }
     dst += tstep;
+  }
+}
+
+// Lanes of column j (is_j) write column j below the diagonal row dj (this
+// wave's rows, strip order) into the wave's slab; rows <= dj lie in tile 0.
+template <int NW, int RL>
+__device__ __forceinline__ void publish_x(float* __restrict__ xw, const float (&c)[RL], int dj,
+                                          bool is_j, int w, int g) {
+  using S = Strip<NW, RL>;
+  if (is_j) {
+    f32x4 xv;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) xv[v] = (S::row(0, v, w, g) > dj) ? c[v] : 0.0f;
+    *reinterpret_cast<f32x4*>(&xw[4 * g]) = xv;
+#pragma unroll
+    for (int t = 1; t < S::kTiles; ++t) {  // rows >= r hold zeros
+      const f32x4 cv = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
+      *reinterpret_cast<f32x4*>(&xw[16 * t + 4 * g]) = cv;
+    }
   }
 }
 
@@ -249,9 +272,10 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   using S = Strip<NW, RL>;
   __shared__ WyShared<NW, RL> wy;
   __shared__ __align__(16) float xs[NW][4 * RL];
-  __shared__ float red[2][NW][16];
+  // Row stride 4 NW + 4: the b128 reads of 16 columns land on distinct banks.
+  __shared__ __align__(16) float red[2][16][4 * NW + 4];
   __shared__ float erow[2][16];
-  __shared__ float zbuf[16][17];
+  __shared__ __align__(16) float zbuf[16][16];
   __shared__ float tbuf[16][17];
   __shared__ float taus[16];
   __shared__ float scr[2][NW];
@@ -274,43 +298,46 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   const int d0 = 16 * p;
   float my_beta = 0.0f, my_gamma = 1.0f, my_pre = 1.0f, my_tau = 0.0f;
   float* xw = xs[w];
+  // Small strips keep x in registers between the dot and the update.
+  constexpr bool kKeepX = RL <= 32;
+  constexpr int RX = kKeepX ? RL : 1;
 
+  // x for step 0; later steps are published by the lanes of column j+1 right
+  // after their update of step j, so the write is off the critical path.
+  publish_x<NW, RL>(xw, c, d0, k == 0, w, g);
   for (int j = 0; j < kw; ++j) {
     const int dj = d0 + j;
-    __builtin_amdgcn_wave_barrier();
-    // Lanes of column j publish x = column j below the diagonal (this wave's rows).
-    if (k == j) {
-      // Rows <= dj < 16 NW all sit in tile 0, so only tile 0 is masked.
-      f32x4 xv;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) xv[v] = (S::row(0, v, w, g) > dj) ? c[v] : 0.0f;
-      *reinterpret_cast<f32x4*>(&xw[4 * g]) = xv;
-#pragma unroll
-      for (int t = 1; t < S::kTiles; ++t) {
-        if (S::tile_row0(t, w) >= r) break;
-        const f32x4 cv = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
-        *reinterpret_cast<f32x4*>(&xw[16 * t + 4 * g]) = cv;
-      }
-    }
     if (w == p && g == (j >> 2)) {
       const int v = j & 3;
       erow[j & 1][k] = (v == 0) ? c[0] : (v == 1) ? c[1] : (v == 2) ? c[2] : c[3];
     }
     wave_sync();
-    float d = 0.0f;
+    float x[RX];
+    float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < S::kTiles; ++t) {
-      if (S::tile_row0(t, w) >= r) continue;
       const f32x4 xv = *reinterpret_cast<const f32x4*>(&xw[16 * t + 4 * g]);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) d = fmaf(xv[v], c[4 * t + v], d);
+      for (int v = 0; v < 4; ++v) {
+        if constexpr (kKeepX) x[4 * t + v] = xv[v];
+        dv[v] = fmaf(xv[v], c[4 * t + v], dv[v]);
+      }
     }
-    d = sum_over_rows16(d);
-    if (g == 0) red[j & 1][w][k] = d;
+    // Partial dot of (wave w, row group g) for column k, summed after the barrier.
+    red[j & 1][k][4 * w + g] = (dv[0] + dv[1]) + (dv[2] + dv[3]);
     __syncthreads();
-    float ds = 0.0f;
+    float ds;
+    {
+      const float* rp = red[j & 1][k];
+      f32x4 a4 = *reinterpret_cast<const f32x4*>(rp);
 #pragma unroll
-    for (int u = 0; u < NW; ++u) ds += red[j & 1][u][k];
+      for (int u = 1; u < NW; ++u) {
+        const f32x4 q4 = *reinterpret_cast<const f32x4*>(rp + 4 * u);
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) a4[e4] += q4[e4];
+      }
+      ds = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+    }
     const float e = erow[j & 1][k];
     const float sigma = readlane_f(ds, j);
     const float alpha = readlane_f(e, j);
@@ -322,13 +349,10 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
     } else if (reflector_fast_ok(alpha, sigma)) {
       R = reflector_fast(alpha, sigma);
     } else {
-      // Scaled norm of x from the per-wave slabs: two workgroup reductions.
-      // Only tiles holding rows < r were published this step.
-      int nvalid = 0;
-#pragma unroll
-      for (int t = 0; t < S::kTiles; ++t) nvalid += (S::tile_row0(t, w) < r) ? 16 : 0;
+      // Rare path (zero, tiny or huge column): scaled norm of x from the slab,
+      // two workgroup reductions.
       float xm = 0.0f;
-      for (int idx = lane; idx < nvalid; idx += 64) xm = fmaxf(xm, fabsf(xw[idx]));
+      for (int idx = lane; idx < 4 * RL; idx += 64) xm = fmaxf(xm, fabsf(xw[idx]));
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) xm = fmaxf(xm, __shfl_xor(xm, o));
       if (lane == 0) scr[0][w] = xm;
@@ -336,16 +360,16 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       float xmax = 0.0f;
 #pragma unroll
       for (int u = 0; u < NW; ++u) xmax = fmaxf(xmax, scr[0][u]);
-      float s = 0.0f;
+      float sq = 0.0f;
       if (xmax > 0.0f) {
-        for (int idx = lane; idx < nvalid; idx += 64) {
+        for (int idx = lane; idx < 4 * RL; idx += 64) {
           const float tq = xw[idx] / xmax;
-          s = fmaf(tq, tq, s);
+          sq = fmaf(tq, tq, sq);
         }
       }
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
-      if (lane == 0) scr[1][w] = s;
+      for (int o = 1; o < 64; o <<= 1) sq += __shfl_xor(sq, o);
+      if (lane == 0) scr[1][w] = sq;
       __syncthreads();
       float ssq = 0.0f;
 #pragma unroll
@@ -361,14 +385,18 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       const float cc = R.tau * wk;
       // fast: c -= (cc gamma) x;  slow: c -= cc ((x pre) gamma)
       const float cx = upd ? (fast ? cc * R.gamma : cc) : 0.0f;
+      if (fast && kKeepX) {
 #pragma unroll
-      for (int t = 0; t < S::kTiles; ++t) {
-        if (S::tile_row0(t, w) >= r) continue;
-        const f32x4 xv = *reinterpret_cast<const f32x4*>(&xw[16 * t + 4 * g]);
+        for (int m = 0; m < RX; ++m) c[m] = fmaf(-cx, x[m], c[m]);
+      } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float xe = fast ? xv[v] : (xv[v] * R.pre) * R.gamma;
-          c[4 * t + v] = fmaf(-cx, xe, c[4 * t + v]);
+        for (int t = 0; t < S::kTiles; ++t) {
+          const f32x4 xv = *reinterpret_cast<const f32x4*>(&xw[16 * t + 4 * g]);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float xe = fast ? xv[v] : (xv[v] * R.pre) * R.gamma;
+            c[4 * t + v] = fmaf(-cx, xe, c[4 * t + v]);
+          }
         }
       }
       if (upd && own_row) {
@@ -388,23 +416,37 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       my_pre = R.pre;
       my_tau = R.tau;
     }
+    // x for step j+1 (every lane of this wave has finished reading the slab).
+    if (j + 1 < kw) publish_x<NW, RL>(xw, c, dj + 1, k == j + 1, w, g);
   }
   if (w == 0 && g == 0) taus[k] = (k < kw) ? my_tau : 0.0f;
   __syncthreads();
 
   // T_p (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
-  // Lane k of wave 0 holds row k of T in registers; z_j is read as broadcasts.
+  // Lane k of wave 0 holds row k of T in registers; z_j rows are b128 reads.
   if (w == 0 && g == 0) {
     float trow[16];
+    const float tk = taus[k];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) trow[q] = 0.0f;
+    for (int q = 0; q < 16; ++q) trow[q] = (q == k) ? tk : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float s = 0.0f;
+    for (int j = 1; j < 16; ++j) {
+      float z[16];
 #pragma unroll
-      for (int q = 0; q < j; ++q) s = fmaf(trow[q], zbuf[j][q], s);  // trow[q] = 0 for q < k
+      for (int q4 = 0; q4 < (j + 3) / 4; ++q4) {
+        const f32x4 zz = *reinterpret_cast<const f32x4*>(&zbuf[j][4 * q4]);
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) z[4 * q4 + e4] = zz[e4];
+      }
+      float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+      for (int q = 0; q < j; ++q) {  // trow[q] = 0 for q < k
+        if (q & 1) sb = fmaf(trow[q], z[q], sb);
+        else sa = fmaf(trow[q], z[q], sa);
+      }
       const float tj = taus[j];
-      trow[j] = (j >= kw) ? 0.0f : ((k < j) ? -tj * s : ((k == j) ? tj : 0.0f));
+      // zbuf rows j >= kw are not written by this launch: never read them.
+      trow[j] = (j < kw && k < j) ? -tj * (sa + sb) : trow[j];
     }
     float* Tp = Tb + 256 * p;
 #pragma unroll

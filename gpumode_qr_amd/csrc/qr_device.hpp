@@ -37,14 +37,22 @@ __device__ __forceinline__ bool reflector_fast_ok(float alpha, float sigma) {
   return sigma >= kSigmaLo && sigma <= kSigmaHi && fabsf(alpha) <= kAlphaHi;
 }
 
-// Fast path: sigma = sum(x^2) in [2^-100, 2^100], |alpha| <= 2^50.
+// 1/x from v_rcp_f32 plus one Newton step (about 0.5 ulp) for normal x.
+__device__ __forceinline__ float rcp_nr(float x) {
+  const float r = __builtin_amdgcn_rcpf(x);
+  return fmaf(r, fmaf(-x, r, 1.0f), r);
+}
+
+// Fast path: sigma = sum(x^2) in [2^-100, 2^100], |alpha| <= 2^50, so every
+// operand below is a normal number; v_sqrt_f32 (1 ulp) and rcp_nr replace the
+// IEEE divide/sqrt expansions, which sit on the per-column latency chain.
 __device__ __forceinline__ Reflector reflector_fast(float alpha, float sigma) {
   Reflector r;
-  const float norm = sqrtf(fmaf(alpha, alpha, sigma));
+  const float norm = __builtin_amdgcn_sqrtf(fmaf(alpha, alpha, sigma));
   const float beta = -copysignf(norm, alpha);
   r.beta = beta;
-  r.tau = (beta - alpha) / beta;
-  r.gamma = 1.0f / (alpha - beta);
+  r.tau = (beta - alpha) * rcp_nr(beta);
+  r.gamma = rcp_nr(alpha - beta);
   r.pre = 1.0f;
   return r;
 }
