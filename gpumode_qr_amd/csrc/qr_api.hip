@@ -51,6 +51,7 @@ size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 // the current outer block.
 size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kTStride * sizeof(float)); }
 
+
 // Panels per outer block for size n (QR_OUTER_BLOCKS=1..8 overrides).
 int outer_blocks(int n) {
   if (const char* env = std::getenv("QR_OUTER_BLOCKS")) {
@@ -169,13 +170,57 @@ hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, i
   });
 }
 
-hipError_t run_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int ncols,
-                     const float* T, int64_t sTb, int batch, hipStream_t s) {
-  const double flops = 4.0 * r * kPanel * (double)ncols * nblk * batch;
-  const double bytes = (2.0 * r * ncols + (double)r * kPanel * nblk) * 4.0 * batch;
+// Columns c0 .. c0+ncols-1 (relative to the outer block at J0) := Q^T C.
+hipError_t run_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
+                     int ncols, const float* T, int64_t sTb, int batch, hipStream_t s) {
+  double rows = 0.0;  // sum over the blocks of their row counts
+  for (int q = 0; q < nblk; ++q) rows += r - kPanel * q;
+  const double flops = 4.0 * kPanel * (double)ncols * rows * batch;
+  const double bytes = (2.0 * r * ncols + rows * kPanel) * 4.0 * batch;
   return traced(QR_KERNEL_TRAIL, flops, bytes, s, [&] {
-    return qr::launch_trail(H, sHb, ldh, J0, nblk, r, kPanel * nblk, ncols, T, sTb, batch, s);
+    return qr::launch_trail(H, sHb, ldh, J0, nblk, r, c0, ncols, T, sTb, batch, s);
   });
+}
+
+// Second stream (default priority) and two events per device for the
+// look-ahead schedule of qr_geqrf_f32; created on first use, kept for the
+// life of the process.
+struct Lookahead {
+  hipStream_t s2 = nullptr;
+  hipEvent_t panels_done = nullptr;
+  hipEvent_t rest_done = nullptr;
+};
+
+std::mutex g_la_mu;
+std::vector<Lookahead> g_la;
+
+bool lookahead_for_current_device(Lookahead* out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return false;
+  std::lock_guard<std::mutex> lk(g_la_mu);
+  if ((int)g_la.size() <= dev) g_la.resize(dev + 1);
+  Lookahead& la = g_la[dev];
+  if (!la.s2) {
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return false;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
+      hipStreamDestroy(st);
+      return false;
+    }
+    la.s2 = st;
+    la.panels_done = a;
+    la.rest_done = b;
+  }
+  *out = la;
+  return true;
+}
+
+// Look-ahead on/off (QR_LOOKAHEAD=0 disables it).
+bool lookahead_enabled() {
+  const char* env = std::getenv("QR_LOOKAHEAD");
+  return !(env && env[0] == '0');
 }
 
 }  // namespace
@@ -199,7 +244,7 @@ int qr_max_n(void) { return kMaxN; }
 
 size_t qr_geqrf_f32_workspace(int batch, int n) {
   if (batch <= 0 || n <= kSmallN || n > kMaxN) return 0;
-  return ws_t_bytes(batch);
+  return 2 * ws_t_bytes(batch);
 }
 
 int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
@@ -220,14 +265,31 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
 
   const size_t need = qr_geqrf_f32_workspace(batch, n);
   if (workspace_bytes < need || !workspace) return QR_EWORKSPACE;
-  float* Tws = static_cast<float*>(workspace);
+  // Two T slots per matrix: outer block k uses slot k & 1, so the panels of
+  // block k+1 never overwrite T factors that block k's trailing update reads.
+  float* Tslot[2] = {static_cast<float*>(workspace),
+                     static_cast<float*>(workspace) + (size_t)batch * kTStride};
 
   hipError_t e = traced(QR_KERNEL_COPY, 0.0, 2.0 * nn * 4.0 * batch, s, [&] {
     return qr::launch_copy_in(A, sAb, sAr, sAc, H, nn, batch, n, s);
   });
   if (e != hipSuccess) return QR_ELAUNCH;
   const int P = outer_blocks(n);
-  for (int J0 = 0; J0 < n; J0 += kPanel * P) {
+  const int NB = kPanel * P;
+
+  // Look-ahead schedule. On the caller's stream s: the panels of block k, then
+  // the update of block k+1's columns only, then the panels of block k+1. On s2:
+  // the update of every column right of block k+1, which runs concurrently
+  // with the panels of block k+1. Events order the two streams:
+  //   s2 waits for "panels of block k done" before updating with them;
+  //   s waits for "rest of block k done" before touching columns >= J0 + 2 NB.
+  Lookahead la;
+  const bool use_la = lookahead_enabled() && n > 2 * NB && lookahead_for_current_device(&la);
+  bool rest_pending = false;  // s2 holds work that s must wait for
+
+  int blk = 0;
+  for (int J0 = 0; J0 < n; J0 += NB, ++blk) {
+    float* Tws = Tslot[blk & 1];
     const int r = n - J0;
     const int nblk = (r + kPanel - 1) / kPanel < P ? (r + kPanel - 1) / kPanel : P;
     for (int p = 0; p < nblk; ++p) {
@@ -236,11 +298,32 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
       if (e != hipSuccess) return QR_ELAUNCH;
     }
     const int ncols = r - kPanel * nblk;
-    if (ncols > 0) {
-      e = run_trail(H, nn, n, J0, nblk, r, ncols, Tws, kTStride, batch, s);
+    if (ncols <= 0) continue;
+    if (!use_la) {
+      e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, ncols, Tws, kTStride, batch, s);
       if (e != hipSuccess) return QR_ELAUNCH;
+      continue;
     }
+    const int next = ncols < NB ? ncols : NB;
+    const int rest = ncols - next;
+    // Columns of block k+1 were last updated by the rest-update of block k-1.
+    if (rest_pending) {
+      if (hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;
+      rest_pending = false;
+    }
+    if (rest > 0) {
+      if (hipEventRecord(la.panels_done, s) != hipSuccess) return QR_ELAUNCH;
+      if (hipStreamWaitEvent(la.s2, la.panels_done, 0) != hipSuccess) return QR_ELAUNCH;
+      e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk + next, rest, Tws, kTStride, batch,
+                    la.s2);
+      if (e != hipSuccess) return QR_ELAUNCH;
+      if (hipEventRecord(la.rest_done, la.s2) != hipSuccess) return QR_ELAUNCH;
+      rest_pending = true;
+    }
+    e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, next, Tws, kTStride, batch, s);
+    if (e != hipSuccess) return QR_ELAUNCH;
   }
+  if (rest_pending && hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;
   return QR_OK;
 }
 
@@ -283,8 +366,8 @@ int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int nblk, int r
       sTb < (int64_t)kPanel * kPanel * nblk)
     return QR_EINVAL;
   if (r > kMaxN) return QR_EUNSUPPORTED;
-  return to_status(
-      run_trail(H, sHb, ldh, j0, nblk, r, c, T, sTb, batch, static_cast<hipStream_t>(stream)));
+  return to_status(run_trail(H, sHb, ldh, j0, nblk, r, kPanel * nblk, c, T, sTb, batch,
+                             static_cast<hipStream_t>(stream)));
 }
 
 int qr_trace_enable(unsigned kernel_mask) {

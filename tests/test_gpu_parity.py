@@ -280,6 +280,31 @@ def test_input_not_modified_and_repeatable():
     assert torch.equal(H1, H2) and torch.equal(t1, t2)
 
 
+@pytest.mark.parametrize("n,batch", [(300, 3), (1100, 2)])
+def test_lookahead_schedule_is_bitwise_identical(monkeypatch, n, batch):
+    # The look-ahead schedule only splits the trailing update into disjoint
+    # column ranges on two streams: results must not change by a single bit.
+    _say(f"look-ahead on/off n={n}")
+    A = _gauss(batch, n, seed=n + 1).to(DEV)
+    monkeypatch.setenv("QR_LOOKAHEAD", "0")
+    H0, t0 = hip_qr.geqrf(A)
+    torch.cuda.synchronize()
+    monkeypatch.setenv("QR_LOOKAHEAD", "1")
+    H1, t1 = hip_qr.geqrf(A)
+    torch.cuda.synchronize()
+    assert torch.equal(H0, H1) and torch.equal(t0, t1)
+
+
+@pytest.mark.parametrize("P", [1, 2, 3, 8])
+def test_outer_block_widths(monkeypatch, oracle, P):
+    _say(f"outer block of {P} panels, n=400")
+    monkeypatch.setenv("QR_OUTER_BLOCKS", str(P))
+    A = _gauss(2, 400, seed=P)
+    H, tau = _run(A)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"P={P}")
+
+
 def test_variant_registry_runs_hip_path():
     from gpumode_qr_amd.variants import CHAMPION, VARIANTS
 
