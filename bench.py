@@ -19,7 +19,9 @@ Also reported:
   algorithmic flops (or bytes) per launch over its mean HIP-event duration,
   recorded on the stream the kernel is launched on (library launch tracer);
 - cpu_baseline: torch.geqrf on the host's CPU cores, on a bounded sample of
-  each config's batch (same inputs), scaled to the full batch.
+  each config's batch (same inputs), scaled to the full batch;
+- rocm_torch_geqrf: torch.geqrf on the same GPU (rocSOLVER), full batch, same
+  inputs, timed live, and the published champion medians at the nearest shapes.
 """
 
 from __future__ import annotations
@@ -41,6 +43,11 @@ METRIC = "geomean median ms (cfg 2-5); GFLOP/s (4/3·n³·b) & % MI355X FP32 pea
 
 # Matrices per config factored by the CPU baseline (bounded sample).
 CPU_SAMPLE = {1: 64, 2: 256, 3: 16, 4: 4, 5: 1}
+
+# Published MI350X medians of the reference's Triton champion at the nearest
+# shapes (cfg 2's stand-in is b256 n64): db/20260708T044736Z_hh_panel_tuned.json:169,
+# db/grid_search_cond1_geqrf_vs_champion.json:3921,3105,2085.
+CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
 
 def _ms_events(fn, A, torch):
@@ -164,6 +171,32 @@ def cpu_baseline(cfgs: list[int], torch) -> dict:
     }
 
 
+def rocm_geqrf(cfgs: list[int], torch) -> dict:
+    """torch.geqrf on the GPU (the reference's torch_geqrf variant) on each
+    config's full batch: one warm-up, then the median of a few event-timed calls."""
+    from gpumode_qr_amd import bench, inputs
+
+    per_cfg = {}
+    for cfg in cfgs:
+        prob = inputs.make_config_problem(cfg, device="cuda")
+        A = prob.tensor
+        torch.geqrf(A)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        times = [_ms_events(torch.geqrf, A, torch)]
+        # Keep the leg bounded: about 3 s per config.
+        reps = max(0, min(4, int(3.0 / max(time.perf_counter() - t0, 1e-3))))
+        times += [_ms_events(torch.geqrf, A, torch) for _ in range(reps)]
+        med = statistics.median(times)
+        per_cfg[cfg] = {"median_ms": med, "calls": len(times)}
+        print(f"[rocm] cfg{cfg}: torch.geqrf median {med:.3f} ms over {len(times)} calls",
+              flush=True)
+        del A
+        torch.cuda.empty_cache()
+    return {"geomean_ms": bench.geomean([v["median_ms"] for v in per_cfg.values()]),
+            "per_config": per_cfg}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -171,6 +204,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-rocm-geqrf", action="store_true",
+                    help="skip timing torch.geqrf on the GPU")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -219,6 +254,16 @@ def main() -> int:
         "share_of_traced_time": dom_ms / sum(totals.values()),
     })
 
+    rocm = None if args.no_rocm_geqrf else rocm_geqrf(cfgs, torch)
+    if rocm is not None:
+        rocm["speedup_vs_torch_geqrf"] = rocm["geomean_ms"] / gm
+    champ = [CHAMPION_PROXY_MS[c] for c in cfgs if c in CHAMPION_PROXY_MS]
+    champion = None
+    if len(champ) == len(cfgs):
+        champion = {"geomean_ms": bench.geomean(champ), "per_config_ms": CHAMPION_PROXY_MS,
+                    "speedup": bench.geomean(champ) / gm,
+                    "note": "published MI350X medians of the Triton champion at the nearest "
+                            "shapes (cfg 2: b256 n64); not measured here"}
     cpu = None if args.no_cpu else cpu_baseline(cfgs, torch)
     out = {
         "metric": METRIC,
@@ -245,6 +290,8 @@ def main() -> int:
         },
         "roofline": roof,
         "cpu_baseline": cpu,
+        "rocm_torch_geqrf": rocm,
+        "champion_proxy": champion,
     }
     print(json.dumps(out), flush=True)
     return 0 if out["config"]["all_gates_pass"] else 3

@@ -467,20 +467,37 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   store_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
 }
 
+// The dispatcher hands workgroup i to XCD i mod kXcds, and each XCD has its
+// own L2. Renumber so that each XCD receives a contiguous range of logical
+// ids, in dispatch order: the strips of one matrix then run on one XCD, close
+// in time, and share its V block and the 128-byte lines of neighbouring
+// strips through that L2 instead of fetching them once per XCD.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int xcd_logical_id(int id, int total) {
+  const int xcd = id % kXcds, slot = id / kXcds;
+  const int q = total / kXcds, rem = total % kXcds;
+  return xcd * q + (xcd < rem ? xcd : rem) + slot;
+}
+
 // Columns c0.. c0+ncols-1 (relative to the outer block at J0, r rows) :=
 // Q^T C with the nblk 16-wide reflector blocks of the outer block, applied
-// in order 0..nblk-1. Grid (ceil(ncols / 16), batch); one strip per workgroup.
+// in order 0..nblk-1. 1-D grid of nstrips * batch workgroups, nstrips =
+// ceil(ncols / 16); one strip per workgroup, strip-major within a matrix
+// after the XCD renumbering.
 template <int NW, int RL>
 __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_t sHb,
                                                    int64_t ldh, int J0, int nblk, int r, int c0,
                                                    int ncols, const float* __restrict__ Tws,
                                                    int64_t sTwb) {
   __shared__ WyShared<NW, RL> wy;
-  const int b = blockIdx.y;
+  const int nstrips = (ncols + 15) / 16;
+  const int id = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int b = id / nstrips;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
-  const int s0 = 16 * blockIdx.x;
+  const int s0 = 16 * (id - b * nstrips);
   float* P = Blk + c0 + s0;
   const float* Tb = Tws + (int64_t)b * sTwb;
   const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
@@ -531,7 +548,9 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
   if (ncols <= 0) return hipSuccess;
   if (nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || r < 16 * (nblk - 1) + 1)
     return hipErrorInvalidValue;
-  const dim3 grid((ncols + 15) / 16, batch);
+  const int64_t wgs = (int64_t)((ncols + 15) / 16) * batch;
+  if (wgs > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)wgs);
 #define QR_TRAIL_CASE(NWV, RLV)                                                              \
   hipLaunchKernelGGL((k_trail<NWV, RLV>), grid, dim3(64 * NWV), 0, stream, H, sHb, ldh, J0, \
                      nblk, r, c0, ncols, Tws, sTwb)
