@@ -49,6 +49,14 @@ CPU_SAMPLE = {1: 64, 2: 256, 3: 16, 4: 4, 5: 1}
 # db/grid_search_cond1_geqrf_vs_champion.json:3921,3105,2085.
 CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
+# Measured HBM MiB (read + write) per geqrf call of the trailing-update kernel
+# k_trail, per config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
+# ``python -m gpumode_qr_amd.profile_run --config C --calls 3``, each scaled by
+# the same counter's reading for k_copy_in of known size (FETCH x2.000, WRITE
+# x1.000). Counters cannot be read from inside this process; rerun those
+# commands after changing the kernel.
+TRAIL_HBM_MIB_PER_CALL = {3: 2362.7 + 1684.6, 4: 1660.6 + 1360.3, 5: 3258.6 + 2728.0}
+
 
 def _ms_events(fn, A, torch):
     s = torch.cuda.Event(enable_timing=True)
@@ -245,9 +253,16 @@ def main() -> int:
         achieved = dom_flops / (dom_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s"}
+    traffic = None
+    if dom == "trail" and all(c in TRAIL_HBM_MIB_PER_CALL for c in cfgs if c != 2):
+        reps = max(1, min(args.steps, 5))
+        per_call = sum(r["kernels"]["trail"]["launches"] for r in rows) / reps
+        traffic = sum(TRAIL_HBM_MIB_PER_CALL[c] for c in cfgs if c != 2) * 2**20 / per_call
     roof.update({
         "frac": roof["achieved"] / roof["peak"],
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
+        "algorithmic_bytes_per_launch": dom_bytes / max(launches, 1),
         "kernel": dom,
         "launches": launches,
         "mean_launch_us": dom_ms * 1e3 / max(launches, 1),
