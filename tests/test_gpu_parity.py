@@ -305,6 +305,20 @@ def test_outer_block_widths(monkeypatch, oracle, P):
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"P={P}")
 
 
+@pytest.mark.parametrize("n", [48, 200])
+def test_tau_range_and_zero_columns(n):
+    _say(f"tau range n={n}")
+    g = torch.Generator().manual_seed(n)
+    A = torch.randn(6, n, n, generator=g)
+    A[2, :, n // 3] = 0.0
+    H, tau = hip_qr.geqrf(A.to(DEV))
+    tau = tau.cpu()
+    nz = tau[tau != 0]
+    assert bool(((nz >= 1 - 1e-6) & (nz <= 2 + 1e-6)).all())
+    assert tau[2, n // 3] == 0 and bool((tau[:, -1] == 0).all())
+    assert nz.numel() == tau.numel() - 7
+
+
 def test_variant_registry_runs_hip_path():
     from gpumode_qr_amd.variants import CHAMPION, VARIANTS
 

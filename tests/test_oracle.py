@@ -109,6 +109,20 @@ def test_oracle_slarfg_closed_form(oracle, scale, alpha_kind):
     np.testing.assert_allclose(v, v_r, rtol=1e-5, atol=1e-6)
 
 
+def test_oracle_tau_range(oracle):
+    # tau = 1 - alpha / beta with |beta| >= |alpha| and sign(beta) = -sign(alpha),
+    # so every tau lies in [1, 2], or is exactly 0 when the column below the
+    # diagonal is already zero (here column 5 of matrix 1 and every last column).
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal((4, 50, 50)).astype(np.float32)
+    A[1, :, 5] = 0.0
+    _, tau = oracle.geqrf(A, nb=16)
+    nz = tau[tau != 0]
+    assert np.all(nz >= 1 - 1e-6) and np.all(nz <= 2 + 1e-6)
+    assert tau[1, 5] == 0 and np.all(tau[:, -1] == 0)
+    assert nz.size == tau.size - 5
+
+
 def test_oracle_slarfg_degenerate(oracle):
     beta, v, tau = oracle.slarfg(2.0, np.zeros(5, np.float32))
     assert (beta, tau) == (2.0, 0.0) and np.all(v == 0.0)
