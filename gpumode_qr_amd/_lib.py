@@ -2,15 +2,18 @@
 
 The library is built in-tree by ``python -m gpumode_qr_amd.csrc.build`` (or
 ``__graft_entry__.build()``). There is no fallback: if the shared library is
-missing, every entry point raises.
+missing, every entry point raises. ``QR_GFX950_LIB`` names another build of
+the same library (for example one built with different tuning defines).
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libqr_gfx950.so"
+DEFAULT_LIB_PATH = Path(__file__).resolve().parent / "libqr_gfx950.so"
+LIB_PATH = Path(os.environ.get("QR_GFX950_LIB") or DEFAULT_LIB_PATH)
 
 # Every symbol include/qr_gfx950.h declares, with (restype, argtypes).
 _i64 = ctypes.c_int64

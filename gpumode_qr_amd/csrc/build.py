@@ -44,9 +44,10 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
 
 
-def _compile(src: str) -> Path:
-    obj = OUT_DIR / (Path(src).stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(src: str, out_dir: Path = OUT_DIR, defines: tuple[str, ...] = ()) -> Path:
+    obj = out_dir / (Path(src).stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-c", str(CSRC / src), "-o",
+           str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
@@ -54,21 +55,30 @@ def _compile(src: str) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    OUT_DIR.mkdir(parents=True, exist_ok=True)
+def build(verbose: bool = False, out: Path = LIB, defines: tuple[str, ...] = ()) -> Path:
+    """Compile and link the library to ``out``; ``defines`` are extra ``-D`` tuning
+    macros (the defaults in the sources are the tuned ones)."""
+    obj_dir = OUT_DIR if out == LIB else OUT_DIR / out.stem
+    obj_dir.mkdir(parents=True, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, obj_dir, defines), SOURCES))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc link failed")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    import argparse
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", type=Path, default=LIB)
+    ap.add_argument("-D", dest="defines", action="append", default=[])
+    a = ap.parse_args()
+    build(verbose=True, out=a.out.resolve(), defines=tuple(a.defines))

@@ -21,8 +21,7 @@
 
 namespace qr {
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
-                               int64_t sHb, float* tau, int64_t sTb, int batch, int n,
-                               hipStream_t stream);
+                               float* tau, int batch, int n, hipStream_t stream);
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
                         float* tau, int64_t sTaub, float* Tws, int64_t sTwb, int batch,
                         hipStream_t stream);
@@ -155,7 +154,7 @@ hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, flo
   const double flops = 4.0 / 3.0 * n * n * (double)n * batch;
   const double bytes = (2.0 * n * n + n) * 4.0 * batch;
   return traced(QR_KERNEL_SMALLN, flops, bytes, s, [&] {
-    return qr::launch_geqrf_smalln(A, sAb, sAr, sAc, H, (int64_t)n * n, tau, n, batch, n, s);
+    return qr::launch_geqrf_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s);
   });
 }
 

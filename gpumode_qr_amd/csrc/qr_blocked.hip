@@ -42,9 +42,12 @@ struct Strip {
 constexpr int kVStride = 20;
 
 // 16-row tiles of V staged per wave at a time (LDS budget: NW * tiles * 1.25 KB).
+#ifndef QR_STAGE_TILES_MAX
+#define QR_STAGE_TILES_MAX 8
+#endif
 template <int NW, int RL>
 struct StageTiles {
-  static constexpr int kMax = NW >= 16 ? 4 : 8;
+  static constexpr int kMax = NW >= 16 ? 4 : QR_STAGE_TILES_MAX;
   static constexpr int value = (RL / 4) < kMax ? (RL / 4) : kMax;
 };
 
@@ -407,9 +410,10 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
         else c[3] -= cc;
       }
     }
-    // Column j of T needs z_k = V_k^T v_j for k < j.
+    // Column j of T needs z_k = V_k^T v_j = ((c_k[j] + (x^T c_k pre) gamma) pre_k)
+    // gamma_k for k < j; pre gamma itself can overflow for tiny columns.
     if (w == 0 && g == 0 && k < j)
-      zbuf[j][k] = (my_pre * my_gamma) * fmaf(R.pre * R.gamma, ds, e);
+      zbuf[j][k] = (fmaf(R.gamma, R.pre * ds, e) * my_pre) * my_gamma;
     if (k == j) {
       my_beta = R.beta;
       my_gamma = R.gamma;

@@ -121,7 +121,9 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 template <int J>
 __device__ __forceinline__ float row_bcast16(float v) {
   static_assert(J >= 0 && J < 16, "row_newbcast lane");
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, false));
+  // Every lane reads a lane of its own row, so no "old" value is ever used:
+  // mov_dpp with bound_ctrl needs no initialising v_mov.
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xF, 0xF, true));
 }
 
 // Same broadcast as a volatile asm: the compiler may not merge two uses into
@@ -147,6 +149,28 @@ __device__ __forceinline__ float max_over_rows16(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   v = fmaxf(v, __shfl_xor(v, 32));
   return v;
+}
+
+// Sum over the four 16-lane rows with the gfx950 permlane swaps (VALU only,
+// no LDS): after permlane32_swap(x, x) the two results hold x[l] and x[l ^ 32]
+// in every lane, after permlane16_swap(y, y) y[l] and y[l ^ 16]. Every lane
+// ends with the same ((x0 + x2) + (x1 + x3)) for its column.
+__device__ __forceinline__ float rows16_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float rows16_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).

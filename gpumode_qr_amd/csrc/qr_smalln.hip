@@ -1,144 +1,440 @@
 // qr_smalln.hip -- kernel (a): fused Householder QR of a whole n x n matrix
-// (n <= 64) per wavefront, geqrf packing.
+// (n <= 64) per wavefront, geqrf packing, with the trailing updates on MFMA.
 //
 // Reference: the fused small-n Triton kernel, src/qrbench/triton_kernels.py:641-755
-// (one program per matrix, per-column reflector + rank-1 trailing update, pack
-// beta on the diagonal and the essential reflector below it).
+// (one program per matrix, per-column reflectors, beta on the diagonal and the
+// essential reflector below it) and its packing/sign rules (:684-719).
 //
-// gfx950 layout: one 64-lane wave per matrix, lane k owns column k in VGPRs
-// (a[NP], NP = n rounded up to 8). Column j is published to LDS by lane j; every
-// lane then forms its dot product with it from its own registers, so the per-step
-// reductions need no cross-lane traffic at all. sigma = x^T x is lane j's own dot
-// and alpha is lane j's row-j entry; both are read back with v_readlane, so the
-// reflector scalars are wave-uniform. Row indices are compile-time (the outer
-// chunk loop is unrolled), so rows above the current chunk are skipped.
+// gfx950 layout: one 64-lane wave holds the whole matrix in VGPRs, padded to
+// NP = 16 S rows and columns (S = ceil(n / 16), zeros outside n x n). Lane l has
+// k = l & 15 (column within a 16-column strip) and g = l >> 4 (row group);
+//   c[s][4 t + v] = A[16 t + 4 g + v][16 s + k],
+// which is the accumulator layout of v_mfma_f32_16x16x4f32 for the 16 x 16 tile
+// (t, s), and also its B-operand layout.
+//
+// Panel p = strip p is factored column by column entirely inside the wave:
+// column j is broadcast to every lane of its 16-lane row with DPP row_newbcast,
+// each lane forms the partial dot of its column over its rows, and the gfx950
+// permlane swaps sum the four row groups. sigma and alpha come back through
+// v_readlane, so the reflector scalars are wave-uniform. The strips right of
+// the panel are then updated as a compact-WY block, C -= V T^T V^T C, with
+// three MFMA chains (W = V^T C, W2 = T^T W, C -= V W2). The only LDS traffic is
+// a wave-private 16 x 16 transpose of V per tile and the T recurrence. No
+// workgroup barrier is used, so waves of a workgroup are independent.
 #include "qr_device.hpp"
 
 namespace qr {
 
-template <int NP, int CH>
-__global__ __launch_bounds__(64) void k_geqrf_smalln(
-    const float* __restrict__ A, int64_t sAb, int64_t sAr, int64_t sAc,
-    float* __restrict__ H, int64_t sHb, float* __restrict__ tau, int64_t sTb, int n) {
-  static_assert(NP % CH == 0 && NP <= 64, "tile");
-  __shared__ __align__(16) float xs[2][NP];
+constexpr int kSnWaves = 4;     // matrices (one per wave) per workgroup
+constexpr int kSnVStride = 20;  // row stride of the V transpose buffer (floats)
 
-  const int b = blockIdx.x;
-  const int k = threadIdx.x;  // column owned by this lane
-  const float* Ab = A + (int64_t)b * sAb;
+template <int S>
+struct SmallnShared {
+  float vt[S * 16 * kSnVStride];  // V tiles of the current panel, row-major
+  float zb[16][16];               // z_j = V[:, 0:j]^T v_j of the current panel
+  float tb[16][17];               // T of the current panel
+  // The panel's registers for the safe re-run; also the 16 x (16 S + 4) staging
+  // tile of the vectorised load.
+  float save[(S * 4 * 64) > 16 * (16 * S + 4) ? (S * 4 * 64) : 16 * (16 * S + 4)];
+};
 
-  float a[NP];
+// Rare path (zero, tiny or huge column, sigma outside [2^-100, 2^100]): the
+// exact power-of-two scaled norm ||x|| = 2^ex sqrt(sum (x 2^-ex)^2), with 2^ex >
+// max |x| from frexp (no term can overflow or lose its significant bits), then
+// slarfg's branches. x0..x15 are this lane's broadcast copies of the pivot
+// column's rows (zeros where the panel has fewer row tiles), so the row-group
+// reductions give the same value in every lane. Out of line: the code exists
+// once instead of once per unrolled column step. Called with all lanes active.
+__device__ __noinline__ Reflector smalln_slow_reflector(
+    float alpha, float x0, float x1, float x2, float x3, float x4, float x5, float x6, float x7,
+    float x8, float x9, float x10, float x11, float x12, float x13, float x14, float x15) {
+  const float x[16] = {x0, x1, x2, x3, x4, x5, x6, x7, x8, x9, x10, x11, x12, x13, x14, x15};
+  float xm = 0.0f;
 #pragma unroll
-  for (int i = 0; i < NP; ++i)
-    a[i] = (i < n && k < n) ? Ab[(int64_t)i * sAr + (int64_t)k * sAc] : 0.0f;
-
-  float my_beta = 0.0f, my_gamma = 1.0f, my_pre = 1.0f, my_tau = 0.0f;
-
-  static_for<0, NP / CH>([&](auto CI) {
-    constexpr int jc = decltype(CI)::value * CH;  // first row/column of this chunk
-    if (jc < n) {
-      for (int jj = 0; jj < CH; ++jj) {
-        const int j = jc + jj;
-        if (j >= n) break;
-        float* x = xs[j & 1];
-        // Lane j publishes x = its column below the diagonal (rows <= j masked).
-        if (k == j) {
+  for (int i = 0; i < 16; ++i) xm = fmaxf(xm, fabsf(x[i]));
+  xm = readlane_f(rows16_max(xm), 0);
+  float scale = 0.0f, ssq = 0.0f;
+  if (xm > 0.0f) {
+    const int ex = __builtin_amdgcn_frexp_expf(xm);
+    float sq = 0.0f;
 #pragma unroll
-          for (int i = jc; i < NP; ++i) x[i] = (i > j) ? a[i] : 0.0f;
-        }
-        __syncthreads();
-        float d = 0.0f;  // x^T a_k over rows > j
-#pragma unroll
-        for (int i = jc; i < NP; ++i) d = fmaf(x[i], a[i], d);
-        float e = 0.0f;  // a_k[j]
-#pragma unroll
-        for (int i = jc; i < jc + CH; ++i) e = (i == j) ? a[i] : e;
-        const float sigma = readlane_f(d, j);
-        const float alpha = readlane_f(e, j);
-
-        Reflector R;
-        bool fast = true;
-        if (j == n - 1) {
-          R = reflector_identity(alpha);
-        } else if (reflector_fast_ok(alpha, sigma)) {
-          R = reflector_fast(alpha, sigma);
-        } else {
-          // Scaled norm of x from the LDS copy (identical in every lane).
-          float xmax = 0.0f;
-#pragma unroll
-          for (int i = jc; i < NP; ++i) xmax = fmaxf(xmax, fabsf(x[i]));
-          float ssq = 0.0f;
-          if (xmax > 0.0f) {
-#pragma unroll
-            for (int i = jc; i < NP; ++i) {
-              const float t = x[i] / xmax;
-              ssq = fmaf(t, t, ssq);
-            }
-          }
-          R = reflector_scaled(alpha, xmax, ssq);
-          fast = false;
-        }
-
-        if (k > j) {
-          // v^T a_k = a_k[j] + sum_{i>j} v_i a_k[i];  a_k -= tau (v^T a_k) v.
-          if (fast) {
-            const float c = R.tau * fmaf(R.gamma, d, e);
-            const float cg = c * R.gamma;
-#pragma unroll
-            for (int i = jc; i < NP; ++i) a[i] = fmaf(-cg, x[i], a[i]);
-#pragma unroll
-            for (int i = jc; i < jc + CH; ++i) a[i] = (i == j) ? a[i] - c : a[i];
-          } else if (R.tau != 0.0f) {
-            const float c = R.tau * fmaf(R.gamma, R.pre * d, e);
-#pragma unroll
-            for (int i = jc; i < NP; ++i) a[i] = fmaf(-c, (x[i] * R.pre) * R.gamma, a[i]);
-#pragma unroll
-            for (int i = jc; i < jc + CH; ++i) a[i] = (i == j) ? a[i] - c : a[i];
-          }
-        }
-        if (k == j) {
-          my_beta = R.beta;
-          my_gamma = R.gamma;
-          my_pre = R.pre;
-          my_tau = R.tau;
-        }
-      }
+    for (int i = 0; i < 16; ++i) {
+      const float q = __builtin_amdgcn_ldexpf(x[i], -ex);
+      sq = fmaf(q, q, sq);
     }
-  });
+    ssq = readlane_f(rows16_sum(sq), 0);
+    scale = __builtin_amdgcn_ldexpf(1.0f, ex);
+  }
+  return reflector_scaled(alpha, scale, ssq);
+}
 
-  if (k < n) {
-    float* Hb = H + (int64_t)b * sHb;
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Per-panel reflector state of this lane's column (column 16 P + k).
+struct SmallnCol {
+  float beta = 0.0f, gamma = 1.0f, pre = 1.0f, tau = 0.0f;
+};
+
+// Column step JJ of panel P (column j = 16 P + JJ): reflector of column j and
+// its application to the panel's columns j+1.. (lanes k > JJ).
+//
+// kSafe = false is the hot path: straight-line code, the fast reflector only
+// (sigma = sum x^2 in [2^-100, 2^100], |alpha| <= 2^50) plus the identity of a
+// column with no rows below the diagonal. A column outside that range clears
+// `ok` and leaves garbage; the caller then restores the panel and re-runs it
+// with kSafe = true, which takes slarfg's general path (zero, tiny, huge) for
+// such columns: v = (x pre) gamma with the power-of-two prescale `pre`.
+template <int S, int P, int JJ, bool kSafe>
+__device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S>& sh, int k0,
+                                            int g0, int n, bool kin, bool& ok,
+                                            SmallnCol& col) {
+  constexpr int NT = S - P;  // row tiles at or below the panel's diagonal tile
+  constexpr int gj = JJ >> 2, vj = JJ & 3;
+  const int j = 16 * P + JJ;
+  // Opaque per-step copies of the lane coordinates: the lane-mask compares
+  // below are formed where they are used instead of being hoisted out of all
+  // the unrolled steps into SGPR pairs.
+  int k = k0, g = g0;
+  asm volatile("" : "+v"(k), "+v"(g));
+  const bool upd = (k > JJ) && kin;
+
+  // x = column j below the diagonal (rows <= j masked), broadcast from lane JJ
+  // of every 16-lane row; partial dot with this lane's column.
+  float xb[NT][4];
+  float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      if (i < n) {
-        const float v = (i < k) ? a[i] : ((i == k) ? my_beta : (a[i] * my_pre) * my_gamma);
-        Hb[(int64_t)i * n + k] = v;
-      }
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float own = c[P][4 * (P + t) + v];
+      if (t == 0) own = (g >= (JJ - v + 4) / 4) ? own : 0.0f;  // row 4 g + v > JJ
+      xb[t][v] = row_bcast16<JJ>(own);
+      dv[v] = fmaf(xb[t][v], c[P][4 * (P + t) + v], dv[v]);
     }
-    tau[(int64_t)b * sTb + k] = my_tau;
+  // sigma and alpha, on the per-column critical path, come straight from the
+  // four partial dots of lane JJ's row groups and from the lane that holds row
+  // j; the per-lane sums over the row groups (needed by every column's update)
+  // run beside them.
+  const float dsum = (dv[0] + dv[1]) + (dv[2] + dv[3]);
+  const float sigma = (readlane_f(dsum, JJ) + readlane_f(dsum, JJ + 32)) +
+                      (readlane_f(dsum, JJ + 16) + readlane_f(dsum, JJ + 48));
+  const float alpha = readlane_f(c[P][4 * P + vj], JJ + 16 * gj);
+  const float ev = (g == gj) ? c[P][4 * P + vj] : 0.0f;  // row j of this column
+  const float ds = rows16_sum(dsum);
+  const float e = rows16_sum(ev);
+  const bool identity = j >= n - 1;  // no rows below the diagonal: tau = 0
+
+  Reflector R;
+  float wk;
+  if constexpr (!kSafe) {
+    ok = ok && (identity || reflector_fast_ok(alpha, sigma));
+    R = reflector_fast(alpha, identity ? 1.0f : sigma);
+    R.beta = identity ? alpha : R.beta;
+    R.tau = identity ? 0.0f : R.tau;
+    R.gamma = identity ? 1.0f : R.gamma;
+    // v^T c_k = c_k[j] + gamma x^T c_k;  c_k -= tau (v^T c_k) v.
+    wk = fmaf(R.gamma, ds, e);
+    const float cc = R.tau * wk;
+    const float cx = upd ? cc * R.gamma : 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        c[P][4 * (P + t) + v] = fmaf(-cx, xb[t][v], c[P][4 * (P + t) + v]);
+    if (upd && g == gj) c[P][4 * P + vj] -= cc;
+  } else {
+    bool fast = true;
+    if (identity) {
+      R = reflector_identity(alpha);
+    } else if (reflector_fast_ok(alpha, sigma)) {
+      R = reflector_fast(alpha, sigma);
+    } else {
+      float xa[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xa[i] = (i < 4 * NT) ? xb[i / 4][i % 4] : 0.0f;
+      R = smalln_slow_reflector(alpha, xa[0], xa[1], xa[2], xa[3], xa[4], xa[5], xa[6], xa[7],
+                                xa[8], xa[9], xa[10], xa[11], xa[12], xa[13], xa[14], xa[15]);
+      fast = false;
+    }
+    // v^T c_k = c_k[j] + ((x^T c_k) pre) gamma;  c_k -= tau (v^T c_k) v with
+    // v = (x pre) gamma. The product pre gamma can overflow (tiny x: pre =
+    // 2^102), so it is never formed.
+    wk = fmaf(R.gamma, R.pre * ds, e);
+    const float cc = R.tau * wk;
+    if (fast) {
+      const float cx = upd ? cc * R.gamma : 0.0f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          c[P][4 * (P + t) + v] = fmaf(-cx, xb[t][v], c[P][4 * (P + t) + v]);
+    } else {
+      const float cx = upd ? cc : 0.0f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          c[P][4 * (P + t) + v] = fmaf(-cx, (xb[t][v] * R.pre) * R.gamma, c[P][4 * (P + t) + v]);
+    }
+    if (upd && g == gj) c[P][4 * P + vj] -= cc;
+  }
+  // Column j of T needs z_q = V_q^T v_j = ((c_q[j] + (x^T c_q pre) gamma) pre_q)
+  // gamma_q for the panel's q < j (c_q still holds the raw x_q). Every row
+  // group stores the same value.
+  sh.zb[JJ][k] = (k < JJ) ? (wk * col.pre) * col.gamma : 0.0f;
+  if (k == JJ) {
+    col.beta = R.beta;
+    col.gamma = R.gamma;
+    col.pre = R.pre;
+    col.tau = R.tau;
   }
 }
 
-// Host-side dispatch over the padded size.
+template <int S, bool kVec>
+__global__ __launch_bounds__(64 * kSnWaves) void k_geqrf_smalln(
+    const float* __restrict__ A, int64_t sAb, int64_t sAr, int64_t sAc, float* __restrict__ H,
+    float* __restrict__ tau, int batch, int n) {
+  __shared__ __align__(16) SmallnShared<S> shm[kSnWaves];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int b = blockIdx.x * kSnWaves + w;
+  if (b >= batch) return;  // whole wave: no workgroup barrier below
+  SmallnShared<S>& sh = shm[w];
+  const int lane = threadIdx.x & 63;
+  const int k0 = lane & 15, g0 = lane >> 4;
+  const int k = k0, g = g0;
+  const float* Ab = A + (int64_t)b * sAb;
+
+  float c[S][4 * S];
+  if constexpr (kVec) {
+    // n = 16 S, unit column stride, 16-byte aligned rows: every lane loads
+    // S^2 16-byte row pieces (16 lanes cover a 64-float row, so each load
+    // instruction reads 4 whole rows), then each 16-row tile is transposed to
+    // the strip layout through LDS (row pitch 16 S + 4: conflict-free reads).
+    static_assert(S == 4, "vectorised load is laid out for 64 x 64");
+    constexpr int kPitch = 16 * S + 4;
+    f32x4 q[S][4];
+#pragma unroll
+    for (int t = 0; t < S; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        q[t][m] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)(16 * t + 4 * m + g) * sAr +
+                                                  4 * k);
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<f32x4*>(&sh.save[(4 * m + g) * kPitch + 4 * k]) = q[t][m];
+      wave_lds_sync();
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) c[s2][4 * t + v] = sh.save[(4 * g + v) * kPitch + 16 * s2 + k];
+      wave_lds_sync();
+    }
+  } else {
+  // Branch-free loads: out-of-range rows/columns read a clamped (valid)
+  // address and are replaced by zero, so the 16 S^2 loads issue back to back.
+  const float* base = Ab + (int64_t)(4 * g) * sAr + (int64_t)k * sAc;
+  static_for<0, S>([&](auto SI) {
+    constexpr int s = decltype(SI)::value;
+    const int col = 16 * s + k;
+    const int64_t coff = (col < n) ? (int64_t)(16 * s) * sAc : -(int64_t)k * sAc;
+#pragma unroll
+    for (int t = 0; t < S; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * t + 4 * g + v;
+        const int64_t roff = (row < n) ? (int64_t)(16 * t + v) * sAr : -(int64_t)(4 * g) * sAr;
+        float val = base[roff + coff];
+        asm volatile("" : "+v"(val));  // keep the load unconditional
+        c[s][4 * t + v] = (row < n && col < n) ? val : 0.0f;
+      }
+  });
+  }
+
+  static_for<0, S>([&](auto PI) {
+    constexpr int p = decltype(PI)::value;
+    constexpr int NT = S - p;  // row tiles at or below the panel's diagonal tile
+    const int kw = min(16, n - 16 * p);  // >= 1: S = ceil(n / 16)
+    const bool kin = k0 < kw;            // this lane's column exists
+
+    // The steps only modify the panel's own rows >= 16 p: keep a copy for the
+    // safe re-run (conflict-free b128 stores, lane-consecutive).
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<f32x4*>(&sh.save[(t * 64 + lane) * 4]) =
+          f32x4{c[p][4 * (p + t)], c[p][4 * (p + t) + 1], c[p][4 * (p + t) + 2],
+                c[p][4 * (p + t) + 3]};
+    SmallnCol col;
+    bool ok = true;
+    static_for<0, 16>([&](auto JI) {
+      constexpr int jj = decltype(JI)::value;
+      if (jj < kw) smalln_step<S, p, jj, false>(c, sh, k0, g0, n, kin, ok, col);
+    });
+    if (!ok) [[unlikely]] {
+      wave_lds_sync();
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(&sh.save[(t * 64 + lane) * 4]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) c[p][4 * (p + t) + v] = sv[v];
+      }
+      col = SmallnCol();
+      bool unused = true;
+      static_for<0, 16>([&](auto JI) {
+        constexpr int jj = decltype(JI)::value;
+        if (jj < kw) smalln_step<S, p, jj, true>(c, sh, k0, g0, n, kin, unused, col);
+      });
+    }
+    const float my_beta = col.beta, my_gamma = col.gamma, my_pre = col.pre, my_tau = col.tau;
+
+    if (g == 0 && k < kw) tau[(int64_t)b * n + 16 * p + k] = my_tau;
+
+    // Final packing of the panel: R above the diagonal, beta on it, the
+    // essential reflector v = (x pre) gamma below it.
+    const int kd = 16 * p + k;
+#pragma unroll
+    for (int t = p; t < S; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * t + 4 * g + v;
+        const float x = c[p][4 * t + v];
+        c[p][4 * t + v] = (row < kd) ? x : ((row == kd) ? my_beta : (x * my_pre) * my_gamma);
+      }
+
+    if constexpr (p + 1 < S) {
+      // T (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
+      // Lane k builds row k in registers; every row group does the same.
+      wave_lds_sync();
+      float trow[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) trow[q] = (q == k) ? my_tau : 0.0f;
+      static_for<1, 16>([&](auto JI) {
+        constexpr int jq = decltype(JI)::value;
+        const float tj = readlane_f(my_tau, jq);
+        float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+        for (int q4 = 0; q4 < (jq + 3) / 4; ++q4) {
+          const f32x4 z = *reinterpret_cast<const f32x4*>(&sh.zb[jq][4 * q4]);
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int q = 4 * q4 + e4;
+            if (q < jq) {
+              if (q & 1) sb = fmaf(trow[q], z[e4], sb);
+              else sa = fmaf(trow[q], z[e4], sa);
+            }
+          }
+        }
+        // Columns jq >= kw do not exist (zb row not written): T stays zero there.
+        if (jq < kw && k < jq) trow[jq] = -tj * (sa + sb);
+      });
+      if (g == 0) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) sh.tb[k][q] = trow[q];
+      }
+
+      // V of the panel, unit lower-trapezoidal: kept in registers for the
+      // A operand of W = V^T C, and staged row-major for the A operand of V W2.
+      float vm[NT][4];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * (p + t) + 4 * g + v;
+          const float x = c[p][4 * (p + t) + v];
+          vm[t][v] = (row < kd) ? 0.0f : ((row == kd) ? 1.0f : x);
+          sh.vt[(16 * t + 4 * g + v) * kSnVStride + k] = vm[t][v];
+        }
+      wave_lds_sync();
+      f32x4 treg, va[NT];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) treg[v] = sh.tb[4 * g + v][k];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        va[t] = *reinterpret_cast<const f32x4*>(&sh.vt[(16 * t + k) * kSnVStride + 4 * g]);
+
+#pragma unroll
+      for (int s = p + 1; s < S; ++s) {
+        // W = V^T C_s (16 reflectors x 16 columns), accumulator layout.
+        f32x4 wacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            wacc = __builtin_amdgcn_mfma_f32_16x16x4f32(vm[t][v], c[s][4 * (p + t) + v], wacc, 0,
+                                                        0, 0);
+        // W2 = T^T W: K slice v pairs T[4g + v][:] with W[4g + v][:].
+        f32x4 w2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          w2 = __builtin_amdgcn_mfma_f32_16x16x4f32(treg[v], wacc[v], w2, 0, 0, 0);
+        // C_s -= V W2: lane (k, g) supplies V[16 t + k][4 g + v] and W2[4 g + v][k].
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          f32x4 acc = {c[s][4 * (p + t)], c[s][4 * (p + t) + 1], c[s][4 * (p + t) + 2],
+                       c[s][4 * (p + t) + 3]};
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-va[t][v], w2[v], acc, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) c[s][4 * (p + t) + v] = acc[v];
+        }
+      }
+      wave_lds_sync();  // sh is rewritten by the next panel
+    }
+  });
+
+  float* Hb = H + (int64_t)b * n * n + (int64_t)(4 * g) * n + k;
+  if (n == 16 * S) {
+    static_for<0, S>([&](auto SI) {
+      constexpr int s = decltype(SI)::value;
+#pragma unroll
+      for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
+    });
+  } else {
+    int kk = k0, gg = g0;
+    asm volatile("" : "+v"(kk), "+v"(gg));
+    static_for<0, S>([&](auto SI) {
+      constexpr int s = decltype(SI)::value;
+#pragma unroll
+      for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (16 * t + 4 * gg + v < n && 16 * s + kk < n)
+            Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
+    });
+  }
+}
+
+// Host-side dispatch over the number of 16-column strips. H is (batch, n, n)
+// contiguous and tau (batch, n) contiguous.
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
-                               int64_t sHb, float* tau, int64_t sTb, int batch, int n,
-                               hipStream_t stream) {
-  const int np = (n + 7) & ~7;
-  const dim3 grid(batch), block(64);
-#define QR_SMALLN_CASE(NPV)                                                                   \
-  case NPV:                                                                                   \
-    hipLaunchKernelGGL((k_geqrf_smalln<NPV, 8>), grid, block, 0, stream, A, sAb, sAr, sAc, H, \
-                       sHb, tau, sTb, n);                                                     \
+                               float* tau, int batch, int n, hipStream_t stream) {
+  if (n < 1 || n > 64 || batch < 1) return hipErrorInvalidValue;
+  const dim3 grid((batch + kSnWaves - 1) / kSnWaves), block(64 * kSnWaves);
+  const bool vec = n == 64 && sAc == 1 && (sAr % 4) == 0 && (sAb % 4) == 0 &&
+                   (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  if (vec) {
+    hipLaunchKernelGGL((k_geqrf_smalln<4, true>), grid, block, 0, stream, A, sAb, sAr, sAc, H,
+                       tau, batch, n);
+    return hipGetLastError();
+  }
+#define QR_SMALLN_CASE(SV)                                                                  \
+  case SV:                                                                                  \
+    hipLaunchKernelGGL((k_geqrf_smalln<SV, false>), grid, block, 0, stream, A, sAb, sAr, sAc, \
+                       H, tau, batch, n);                                                   \
     break;
-  switch (np) {
-    QR_SMALLN_CASE(8)
-    QR_SMALLN_CASE(16)
-    QR_SMALLN_CASE(24)
-    QR_SMALLN_CASE(32)
-    QR_SMALLN_CASE(40)
-    QR_SMALLN_CASE(48)
-    QR_SMALLN_CASE(56)
-    QR_SMALLN_CASE(64)
+  switch ((n + 15) / 16) {
+    QR_SMALLN_CASE(1)
+    QR_SMALLN_CASE(2)
+    QR_SMALLN_CASE(3)
+    QR_SMALLN_CASE(4)
     default:
       return hipErrorInvalidValue;
   }

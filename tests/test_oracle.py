@@ -194,6 +194,17 @@ def test_oracle_passes_gates_on_stress_structures(oracle, n):
         assert res.passed, (prob.name, res.as_dict())
 
 
+@pytest.mark.parametrize("n", [2, 3, 4, 8, 16, 64])
+def test_parity_tolerance_admits_mkl(oracle, n):
+    # The stated parity tolerance must accept any correct fp32 factorisation:
+    # MKL's sgeqrf against the oracle on the same Gaussian matrices.
+    rng = np.random.default_rng(n)
+    A = rng.standard_normal((1500 if n <= 16 else 200, n, n)).astype(np.float32)
+    H, tau = oracle.geqrf(A, nb=16)
+    Hm, tm = torch.geqrf(torch.from_numpy(A))
+    assert_parity(A, Hm.numpy(), tm.numpy(), H, tau, what=f"MKL vs oracle n={n}")
+
+
 def test_gates_catch_a_planted_oracle_mistake(oracle):
     # Plant a plausible bug in the oracle's output (one reflector's tau with the
     # wrong sign, then a transposed R block) and check the FP64 gates reject it.
