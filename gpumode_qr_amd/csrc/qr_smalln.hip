@@ -74,10 +74,37 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-panel reflector state of this lane's column (column 16 P + k).
+// Per-panel reflector state of this lane's column (column 16 P + k), and row k
+// of the panel's compact-WY factor T (16 x 16, upper triangular).
 struct SmallnCol {
   float beta = 0.0f, gamma = 1.0f, pre = 1.0f, tau = 0.0f;
+  float prev_tau = 0.0f;  // tau of the previous column step
+  float trow[16] = {};
 };
+
+// Column JQ of T: T[k][JQ] = -tau_JQ sum_{q < JQ} T[k][q] z_q for k < JQ, with
+// z_q = V_q^T v_JQ stored in zb[JQ] by the lanes q during column step JQ. Run
+// one step later, off that step's critical path; LDS operations of one wave
+// are performed in program order, so the stores are visible.
+template <int S, int JQ>
+__device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShared<S>& sh, int k) {
+  if constexpr (JQ > 0) {
+    float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+    for (int q4 = 0; q4 < (JQ + 3) / 4; ++q4) {
+      const f32x4 z = *reinterpret_cast<const f32x4*>(&sh.zb[JQ][4 * q4]);
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int q = 4 * q4 + e4;
+        if (q < JQ) {
+          if (q & 1) sb = fmaf(col.trow[q], z[e4], sb);
+          else sa = fmaf(col.trow[q], z[e4], sa);
+        }
+      }
+    }
+    col.trow[JQ] = (k < JQ) ? -col.prev_tau * (sa + sb) : col.trow[JQ];
+  }
+}
 
 // Column step JJ of panel P (column j = 16 P + JJ): reflector of column j and
 // its application to the panel's columns j+1.. (lanes k > JJ).
@@ -101,6 +128,7 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   int k = k0, g = g0;
   asm volatile("" : "+v"(k), "+v"(g));
   const bool upd = (k > JJ) && kin;
+  if constexpr (JJ > 0) smalln_t_column<S, JJ - 1>(col, sh, k);
 
   // x = column j below the diagonal (rows <= j masked), broadcast from lane JJ
   // of every 16-lane row; partial dot with this lane's column.
@@ -126,16 +154,17 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   const float ev = (g == gj) ? c[P][4 * P + vj] : 0.0f;  // row j of this column
   const float ds = rows16_sum(dsum);
   const float e = rows16_sum(ev);
-  const bool identity = j >= n - 1;  // no rows below the diagonal: tau = 0
+  // No rows below the diagonal (the last column): tau = 0. (Kept a runtime
+  // test even when n = 16 S is known: the per-step branches keep the
+  // scheduler from hoisting work across steps and raising register pressure.)
+  const bool identity = j >= n - 1;
 
   Reflector R;
   float wk;
   if constexpr (!kSafe) {
     ok = ok && (identity || reflector_fast_ok(alpha, sigma));
-    R = reflector_fast(alpha, identity ? 1.0f : sigma);
-    R.beta = identity ? alpha : R.beta;
-    R.tau = identity ? 0.0f : R.tau;
-    R.gamma = identity ? 1.0f : R.gamma;
+    R = reflector_fast_rcp(alpha, identity ? 1.0f : sigma);
+    if (identity) R = reflector_identity(alpha);
     // v^T c_k = c_k[j] + gamma x^T c_k;  c_k -= tau (v^T c_k) v.
     wk = fmaf(R.gamma, ds, e);
     const float cc = R.tau * wk;
@@ -192,10 +221,14 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     col.pre = R.pre;
     col.tau = R.tau;
   }
+  col.trow[JJ] = (k == JJ) ? R.tau : col.trow[JJ];  // T[JJ][JJ] = tau_JJ
+  col.prev_tau = R.tau;
 }
 
 template <int S, bool kVec>
-__global__ __launch_bounds__(64 * kSnWaves) void k_geqrf_smalln(
+// At least two waves per SIMD (<= 256 VGPRs): 2048 matrices fill every SIMD
+// twice, and the second wave hides the first one's per-column latency.
+__global__ __launch_bounds__(64 * kSnWaves, 2) void k_geqrf_smalln(
     const float* __restrict__ A, int64_t sAb, int64_t sAr, int64_t sAc, float* __restrict__ H,
     float* __restrict__ tau, int batch, int n) {
   __shared__ __align__(16) SmallnShared<S> shm[kSnWaves];
@@ -290,6 +323,11 @@ __global__ __launch_bounds__(64 * kSnWaves) void k_geqrf_smalln(
         if (jj < kw) smalln_step<S, p, jj, true>(c, sh, k0, g0, n, kin, unused, col);
       });
     }
+    // The last column of T (the steps compute each column one step late).
+    static_for<0, 16>([&](auto JI) {
+      constexpr int jq = decltype(JI)::value;
+      if (jq == kw - 1) smalln_t_column<S, jq>(col, sh, k0);
+    });
     const float my_beta = col.beta, my_gamma = col.gamma, my_pre = col.pre, my_tau = col.tau;
 
     if (g == 0 && k < kw) tau[(int64_t)b * n + 16 * p + k] = my_tau;
@@ -307,34 +345,11 @@ __global__ __launch_bounds__(64 * kSnWaves) void k_geqrf_smalln(
       }
 
     if constexpr (p + 1 < S) {
-      // T (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
-      // Lane k builds row k in registers; every row group does the same.
+      // T (16 x 16, upper), row k in lane k: to the accumulator layout via LDS.
       wave_lds_sync();
-      float trow[16];
-#pragma unroll
-      for (int q = 0; q < 16; ++q) trow[q] = (q == k) ? my_tau : 0.0f;
-      static_for<1, 16>([&](auto JI) {
-        constexpr int jq = decltype(JI)::value;
-        const float tj = readlane_f(my_tau, jq);
-        float sa = 0.0f, sb = 0.0f;
-#pragma unroll
-        for (int q4 = 0; q4 < (jq + 3) / 4; ++q4) {
-          const f32x4 z = *reinterpret_cast<const f32x4*>(&sh.zb[jq][4 * q4]);
-#pragma unroll
-          for (int e4 = 0; e4 < 4; ++e4) {
-            const int q = 4 * q4 + e4;
-            if (q < jq) {
-              if (q & 1) sb = fmaf(trow[q], z[e4], sb);
-              else sa = fmaf(trow[q], z[e4], sa);
-            }
-          }
-        }
-        // Columns jq >= kw do not exist (zb row not written): T stays zero there.
-        if (jq < kw && k < jq) trow[jq] = -tj * (sa + sb);
-      });
       if (g == 0) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) sh.tb[k][q] = trow[q];
+        for (int q = 0; q < 16; ++q) sh.tb[k][q] = col.trow[q];
       }
 
       // V of the panel, unit lower-trapezoidal: kept in registers for the
@@ -357,32 +372,48 @@ __global__ __launch_bounds__(64 * kSnWaves) void k_geqrf_smalln(
       for (int t = 0; t < NT; ++t)
         va[t] = *reinterpret_cast<const f32x4*>(&sh.vt[(16 * t + k) * kSnVStride + 4 * g]);
 
+      // The trailing strips s = p+1 .. S-1 are independent: each phase runs
+      // their MFMA chains interleaved, so consecutive MFMAs do not wait on
+      // each other's accumulators.
+      constexpr int NS = S - 1 - p;
+      // W_s = V^T C_s (16 reflectors x 16 columns), accumulator layout.
+      f32x4 wacc[NS];
 #pragma unroll
-      for (int s = p + 1; s < S; ++s) {
-        // W = V^T C_s (16 reflectors x 16 columns), accumulator layout.
-        f32x4 wacc = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int i = 0; i < NS; ++i) wacc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            wacc = __builtin_amdgcn_mfma_f32_16x16x4f32(vm[t][v], c[s][4 * (p + t) + v], wacc, 0,
-                                                        0, 0);
-        // W2 = T^T W: K slice v pairs T[4g + v][:] with W[4g + v][:].
-        f32x4 w2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          w2 = __builtin_amdgcn_mfma_f32_16x16x4f32(treg[v], wacc[v], w2, 0, 0, 0);
-        // C_s -= V W2: lane (k, g) supplies V[16 t + k][4 g + v] and W2[4 g + v][k].
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          f32x4 acc = {c[s][4 * (p + t)], c[s][4 * (p + t) + 1], c[s][4 * (p + t) + 2],
-                       c[s][4 * (p + t) + 3]};
+          for (int i = 0; i < NS; ++i)
+            wacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vm[t][v], c[p + 1 + i][4 * (p + t) + v],
+                                                           wacc[i], 0, 0, 0);
+      // W2_s = T^T W_s: K slice v pairs T[4g + v][:] with W[4g + v][:].
+      f32x4 w2[NS];
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-va[t][v], w2[v], acc, 0, 0, 0);
+      for (int i = 0; i < NS; ++i) w2[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int v = 0; v < 4; ++v) c[s][4 * (p + t) + v] = acc[v];
-        }
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          w2[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(treg[v], wacc[i][v], w2[i], 0, 0, 0);
+      // C_s -= V W2_s: lane (k, g) supplies V[16 t + k][4 g + v] and W2[4 g + v][k].
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f32x4 acc[NS];
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          acc[i] = f32x4{c[p + 1 + i][4 * (p + t)], c[p + 1 + i][4 * (p + t) + 1],
+                         c[p + 1 + i][4 * (p + t) + 2], c[p + 1 + i][4 * (p + t) + 3]};
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int i = 0; i < NS; ++i)
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(-va[t][v], w2[i][v], acc[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) c[p + 1 + i][4 * (p + t) + v] = acc[i][v];
       }
       wave_lds_sync();  // sh is rewritten by the next panel
     }

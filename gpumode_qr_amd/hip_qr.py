@@ -18,6 +18,7 @@ import torch
 from . import _lib
 
 PANEL = 16  # panel width of the blocked route
+SMALL_N = 64  # largest n of the fused one-wave-per-matrix route (no workspace)
 
 
 def _stream(device: torch.device) -> int:
@@ -40,7 +41,12 @@ def workspace_bytes(batch: int, n: int) -> int:
 
 
 def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None):
-    """Batched compact-Householder QR on the GPU: ``(H, tau)`` like torch.geqrf."""
+    """Batched compact-Householder QR on the GPU: ``(H, tau)`` like torch.geqrf.
+
+    The host work between the caller's stream position and the launch is kept
+    small (it is inside every event-timed call): no workspace query for n <= 64,
+    no device switch when ``A`` is on the current device.
+    """
     _check_input(A)
     lib = _lib.load()
     b, n, _ = A.shape
@@ -49,7 +55,7 @@ def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None):
     tau = torch.empty((b, n), dtype=torch.float32, device=dev)
     if b == 0 or n == 0:
         return H, tau
-    need = int(lib.qr_geqrf_f32_workspace(b, n))
+    need = 0 if n <= SMALL_N else int(lib.qr_geqrf_f32_workspace(b, n))
     if need:
         if workspace is None or workspace.numel() * workspace.element_size() < need:
             workspace = torch.empty(need, dtype=torch.uint8, device=dev)
@@ -57,12 +63,14 @@ def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None):
     else:
         ws_ptr, ws_len = None, 0
     sb, sr, sc = A.stride()
-    with torch.cuda.device(dev):
-        st = lib.qr_geqrf_f32(
-            A.data_ptr(), sb, sr, sc, H.data_ptr(), tau.data_ptr(), b, n, ws_ptr, ws_len,
-            _stream(dev),
-        )
-    _lib.check("qr_geqrf_f32", st)
+    args = (A.data_ptr(), sb, sr, sc, H.data_ptr(), tau.data_ptr(), b, n, ws_ptr, ws_len)
+    if dev.index == torch.cuda.current_device():
+        st = lib.qr_geqrf_f32(*args, torch.cuda.current_stream(dev).cuda_stream)
+    else:
+        with torch.cuda.device(dev):
+            st = lib.qr_geqrf_f32(*args, torch.cuda.current_stream(dev).cuda_stream)
+    if st:
+        _lib.check("qr_geqrf_f32", st)
     return H, tau
 
 
