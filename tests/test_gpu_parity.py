@@ -208,6 +208,24 @@ def test_geqrf_known_answers(n):
     assert torch.all(tau[:, -1] == 0)
 
 
+@pytest.mark.parametrize("shape", inputs.BENCHMARK_SHAPES,
+                         ids=[f"b{s['batch']}_n{s['n']}" for s in inputs.BENCHMARK_SHAPES])
+def test_official_shapes(oracle, shape):
+    # The seven ranked GPUMODE shapes (reference inputs.py:20-28): FP64 gates on
+    # the whole batch; elementwise parity with the oracle on two matrices where
+    # the oracle takes seconds (n <= 352).
+    _say(f"official shape b{shape['batch']} n{shape['n']}")
+    prob = inputs.make_benchmark_problem(shape, seed=7, device="cpu")
+    A = prob.tensor
+    H, tau = _run(A)
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+    if shape["n"] <= 352:
+        H_ref, tau_ref = oracle.geqrf(A[:2].numpy(), nb=16)
+        assert_parity(A[:2].numpy(), H[:2].numpy(), tau[:2].numpy(), H_ref, tau_ref,
+                      what=f"n={shape['n']}")
+
+
 @pytest.mark.parametrize("n", [32, 176, 512])
 def test_stress_suite_gates(n):
     for prob in inputs.stress_cases(n=n, batch=4, device="cpu"):
