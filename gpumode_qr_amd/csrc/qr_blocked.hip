@@ -531,6 +531,13 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   }
 
 constexpr int kMaxStripRows = 4096;
+#ifndef QR_TRAIL_WIDE
+#define QR_TRAIL_WIDE 1
+#endif
+#ifndef QR_TRAIL_WIDE_MIN_ROWS
+#define QR_TRAIL_WIDE_MIN_ROWS 512
+#endif
+constexpr int kTrailWideMinRows = QR_TRAIL_WIDE_MIN_ROWS;
 constexpr int kMaxBlocks = 8;
 
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
@@ -558,7 +565,21 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
 #define QR_TRAIL_CASE(NWV, RLV)                                                              \
   hipLaunchKernelGGL((k_trail<NWV, RLV>), grid, dim3(64 * NWV), 0, stream, H, sHb, ldh, J0, \
                      nblk, r, c0, ncols, Tws, sTwb)
+#if QR_TRAIL_WIDE
+  // 16 waves (4 per SIMD) for tall strips: one wave's V staging latency is
+  // covered by the other waves' MFMAs.
+  if (r > kTrailWideMinRows && r <= 512) {
+    QR_TRAIL_CASE(16, 8);
+  } else if (r > 512 && r <= 1024) {
+    QR_TRAIL_CASE(16, 16);
+  } else if (r > 1024 && r <= 2048) {
+    QR_TRAIL_CASE(16, 32);
+  } else {
+    QR_STRIP_DISPATCH(r, QR_TRAIL_CASE)
+  }
+#else
   QR_STRIP_DISPATCH(r, QR_TRAIL_CASE)
+#endif
 #undef QR_TRAIL_CASE
   return hipGetLastError();
 }
