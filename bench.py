@@ -49,13 +49,19 @@ CPU_SAMPLE = {1: 64, 2: 256, 3: 16, 4: 4, 5: 1}
 # db/grid_search_cond1_geqrf_vs_champion.json:3921,3105,2085.
 CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
-# Measured HBM MiB (read + write) per geqrf call of the trailing-update kernel
-# k_trail, per config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
+# Measured HBM MiB (read + write) per geqrf call of each kernel family, per
+# config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
 # ``python -m gpumode_qr_amd.profile_run --config C --calls 3``, each scaled by
 # the same counter's reading for k_copy_in of known size (FETCH x2.000, WRITE
 # x1.000). Counters cannot be read from inside this process; rerun those
-# commands after changing the kernel.
-TRAIL_HBM_MIB_PER_CALL = {3: 2362.7 + 1684.6, 4: 1660.6 + 1360.3, 5: 3258.6 + 2728.0}
+# commands after changing a kernel.
+HBM_MIB_PER_CALL = {
+    "smalln": {2: 33.0 + 33.2},
+    "panel": {3: 1260.6 + 381.3, 4: 429.4 + 140.2, 5: 446.0 + 134.1},
+    "trail": {3: 2362.8 + 1684.6, 4: 1657.0 + 1360.3, 5: 3253.7 + 2741.7},
+    "copy": {3: 640.0 + 640.0, 4: 256.0 + 256.0, 5: 256.0 + 256.0},
+}
+RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
 
 def _ms_events(fn, A, torch):
@@ -246,7 +252,10 @@ def main() -> int:
     dom_ms = sum(r["kernels"][dom]["ms"] for r in rows)
     dom_flops = sum(r["kernels"][dom]["flops"] for r in rows)
     dom_bytes = sum(r["kernels"][dom]["bytes"] for r in rows)
-    if dom in ("smalln", "copy"):
+    # The bound follows the kernel's own arithmetic intensity (algorithmic
+    # flops per algorithmic HBM byte) against the MI355X ridge point.
+    intensity = dom_flops / dom_bytes if dom_bytes > 0 else 0.0
+    if intensity < RIDGE_FLOP_PER_BYTE:
         achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     else:
@@ -254,14 +263,16 @@ def main() -> int:
         roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s"}
     traffic = None
-    if dom == "trail" and all(c in TRAIL_HBM_MIB_PER_CALL for c in cfgs if c != 2):
+    measured = HBM_MIB_PER_CALL.get(dom, {})
+    if cfgs and all(c in measured for c in cfgs if rows[cfgs.index(c)]["kernels"][dom]["launches"]):
         reps = max(1, min(args.steps, 5))
-        per_call = sum(r["kernels"]["trail"]["launches"] for r in rows) / reps
-        traffic = sum(TRAIL_HBM_MIB_PER_CALL[c] for c in cfgs if c != 2) * 2**20 / per_call
+        per_call = sum(r["kernels"][dom]["launches"] for r in rows) / reps
+        traffic = sum(measured.get(c, 0.0) for c in cfgs) * 2**20 / per_call
     roof.update({
         "frac": roof["achieved"] / roof["peak"],
         "traffic": traffic,
         "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
+        "intensity_flop_per_byte": intensity,
         "algorithmic_bytes_per_launch": dom_bytes / max(launches, 1),
         "kernel": dom,
         "launches": launches,
@@ -279,6 +290,23 @@ def main() -> int:
                     "speedup": bench.geomean(champ) / gm,
                     "note": "published MI350X medians of the Triton champion at the nearest "
                             "shapes (cfg 2: b256 n64); not measured here"}
+    # The same roofline figures for every traced kernel family, over all configs.
+    per_kernel = {}
+    for k, ms in totals.items():
+        fl = sum(r["kernels"][k]["flops"] for r in rows)
+        by = sum(r["kernels"][k]["bytes"] for r in rows)
+        n_l = sum(r["kernels"][k]["launches"] for r in rows)
+        inten = fl / by if by > 0 else 0.0
+        if inten < RIDGE_FLOP_PER_BYTE:
+            ach, pk, unit, bnd = by / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", "hbm"
+        else:
+            ach, pk, unit, bnd = fl / (ms * 1e-3) / 1e12, FP32_MFMA_PEAK_TFLOPS, "TFLOP/s", "mfma"
+        per_kernel[k] = {"bound": bnd, "achieved": ach, "unit": unit, "frac": ach / pk,
+                         "intensity_flop_per_byte": inten, "launches": n_l,
+                         "mean_launch_us": ms * 1e3 / max(n_l, 1),
+                         "share_of_traced_time": ms / sum(totals.values())}
+    roof["all_kernels"] = per_kernel
+
     cpu = None if args.no_cpu else cpu_baseline(cfgs, torch)
     out = {
         "metric": METRIC,
