@@ -74,7 +74,8 @@ def _ms_events(fn, A, torch):
     return s.elapsed_time(e)
 
 
-def run_config(cfg: int, steps: int, warmup: int, torch, trace_kernels) -> dict:
+def run_config(cfg: int, steps: int, warmup: int, torch, trace_kernels,
+               with_orgqr: bool = True) -> dict:
     from gpumode_qr_amd import _lib, bench, checker, hip_qr, inputs
 
     prob = inputs.make_config_problem(cfg, device="cuda")
@@ -116,6 +117,16 @@ def run_config(cfg: int, steps: int, warmup: int, torch, trace_kernels) -> dict:
     kernels = {k: _lib.trace_read(k) for k in trace_kernels}
     _lib.trace_reset()
 
+    # Q formation from the same (H, tau) (orgqr, LAPACK flop count 4/3 n^3 per
+    # matrix for a square Q): the step after the factorisation.
+    orgqr_ms = None
+    if with_orgqr:
+        H, tau = fn(A)
+        hip_qr.orgqr(H, tau)
+        torch.cuda.synchronize()
+        orgqr_ms = statistics.median(
+            [_ms_events(lambda x: hip_qr.orgqr(H, tau), A, torch) for _ in range(max(3, steps // 2))])
+        del H, tau
     row = {
         "cfg": cfg,
         "name": prob.name,
@@ -131,10 +142,12 @@ def run_config(cfg: int, steps: int, warmup: int, torch, trace_kernels) -> dict:
         "factor_residual": chk.factor_residual,
         "orth_residual": chk.orth_residual,
         "kernels": kernels,
+        "orgqr_ms": orgqr_ms,
+        "orgqr_tflops": (flops / (orgqr_ms * 1e-3) / 1e12) if orgqr_ms else None,
     }
     print(f"[bench] {prob.name}: median {med:.4f} ms  {row['gflops']:.0f} GFLOP/s "
-          f"({row['pct_fp32_peak']:.2f}% fp32 peak)  {row['hbm_gbs']:.0f} GB/s algorithmic",
-          flush=True)
+          f"({row['pct_fp32_peak']:.2f}% fp32 peak)  {row['hbm_gbs']:.0f} GB/s algorithmic"
+          + (f"  | orgqr {orgqr_ms:.4f} ms" if orgqr_ms else ""), flush=True)
     reps = max(1, min(steps, 5))
     for kname, kv in kernels.items():
         if kv["launches"]:
@@ -220,6 +233,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-rocm-geqrf", action="store_true",
                     help="skip timing torch.geqrf on the GPU")
+    ap.add_argument("--no-orgqr", action="store_true", help="skip timing Q formation (orgqr)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -238,7 +252,8 @@ def main() -> int:
     _lib.load()
     cfgs = [int(c) for c in args.configs.split(",") if c.strip()]
     trace_kernels = ["smalln", "panel", "trail", "copy"]
-    rows = [run_config(c, args.steps, args.warmup, torch, trace_kernels) for c in cfgs]
+    rows = [run_config(c, args.steps, args.warmup, torch, trace_kernels, not args.no_orgqr)
+            for c in cfgs]
     gm = bench.geomean([r["median_ms"] for r in rows])
 
     # Dominant kernel: largest traced time summed over the configs.
@@ -326,7 +341,8 @@ def main() -> int:
                         + ",".join(str(c) for c in cfgs),
             "per_config": [
                 {k: r[k] for k in ("cfg", "name", "batch", "n", "median_ms", "min_ms", "gflops",
-                                   "pct_fp32_peak", "hbm_gbs", "gates_pass")}
+                                   "pct_fp32_peak", "hbm_gbs", "gates_pass", "orgqr_ms",
+                                   "orgqr_tflops")}
                 for r in rows
             ],
             "all_gates_pass": all(r["gates_pass"] for r in rows),

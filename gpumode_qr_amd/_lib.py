@@ -39,6 +39,15 @@ SIGNATURES: dict[str, tuple] = {
         _int,
         [_ptr, _i64, _i64, _int, _int, _ptr, _i64, _ptr, _i64, _i64, _int, _ptr],
     ),
+    "qr_ormqr_f32_workspace": (_size, [_int, _int]),
+    "qr_ormqr_f32": (
+        _int,
+        [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _int, _int, _int, _int, _ptr, _size, _ptr],
+    ),
+    "qr_orgqr_f32": (
+        _int,
+        [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _int, _int, _ptr, _size, _ptr],
+    ),
     "qr_wy_update_f32": (
         _int,
         [_ptr, _i64, _i64, _int, _int, _int, _int, _ptr, _i64, _int, _ptr],
@@ -58,9 +67,9 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 # qr_kernel_id values of include/qr_gfx950.h
-KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4}
+KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4, "apply": 5}
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 QR_OK = 0
 

@@ -32,11 +32,18 @@ hipError_t launch_copy_in(const float* A, int64_t sAb, int64_t sAr, int64_t sAc,
 hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
                         int64_t sTaub, float* T, int64_t sTb, int64_t ldt, int batch,
                         hipStream_t stream);
+hipError_t launch_larft_panels(const float* H, int64_t sHb, int64_t ldh, int n, const float* tau,
+                               int64_t sTaub, float* T, int64_t sTb, int batch,
+                               hipStream_t stream);
+hipError_t launch_apply(const float* V, int64_t sVb, int64_t ldv, float* C, int64_t sCb,
+                        int64_t ldc, int nblk, int r, int ncols, const float* Tws, int64_t sTwb,
+                        bool trans, int kv_last, int batch, hipStream_t stream);
+hipError_t launch_eye(float* Q, int64_t sQb, int64_t ldq, int batch, int n, hipStream_t stream);
 }  // namespace qr
 
 namespace {
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 constexpr int kMaxN = 4096;
 constexpr int kSmallN = 64;
 constexpr int kPanel = 16;
@@ -367,6 +374,96 @@ int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int nblk, int r
   if (r > kMaxN) return QR_EUNSUPPORTED;
   return to_status(run_trail(H, sHb, ldh, j0, nblk, r, kPanel * nblk, c, T, sTb, batch,
                              static_cast<hipStream_t>(stream)));
+}
+
+size_t qr_ormqr_f32_workspace(int batch, int n) {
+  if (batch <= 0 || n <= 0 || n > kMaxN) return 0;
+  return align_up((size_t)batch * ((n + kPanel - 1) / kPanel) * kPanel * kPanel * sizeof(float));
+}
+
+}  // extern "C"
+
+namespace {
+
+// T of every panel (larft from H, tau), then the 16-wide block reflectors in
+// groups of kMaxBlocks panels: Q^T C applies them first to last, Q C last to
+// first. With from_diag, the group starting at row J0 only touches columns
+// J0.. of C (orgqr on the identity: columns left of J0 are unit vectors that
+// are zero in rows J0.., so those blocks leave them unchanged).
+int apply_q(const float* H, int64_t sHb, int64_t ldh, const float* tau, int64_t sTaub, float* C,
+            int64_t sCb, int64_t ldc, int n, int m, bool trans, bool from_diag, int batch,
+            float* Tw, hipStream_t s) {
+  const int np = (n + kPanel - 1) / kPanel;
+  const int64_t sTw = (int64_t)np * kPanel * kPanel;
+  const double lf = (16.0 * 16.0 * n + 16.0 * 16.0 * 16.0 / 3.0) * np * batch;
+  hipError_t e = traced(QR_KERNEL_LARFT, lf, ((double)n * n + n + 256.0 * np) * 4.0 * batch, s,
+                        [&] { return qr::launch_larft_panels(H, sHb, ldh, n, tau, sTaub, Tw, sTw,
+                                                             batch, s); });
+  if (e != hipSuccess) return to_status(e);
+  const int ngroups = (np + kMaxBlocks - 1) / kMaxBlocks;
+  for (int gi = 0; gi < ngroups; ++gi) {
+    const int g = trans ? gi : ngroups - 1 - gi;
+    const int q0 = g * kMaxBlocks;
+    const int nblk = (np - q0) < kMaxBlocks ? (np - q0) : kMaxBlocks;
+    const int J0 = kPanel * q0;
+    const int r = n - J0;
+    const int c0 = from_diag ? J0 : 0;
+    const int ncols = m - c0;
+    const int kv_last = n - kPanel * (q0 + nblk - 1);
+    double rows = 0.0;
+    for (int q = 0; q < nblk; ++q) rows += (double)(r - kPanel * q);
+    const double flops = 4.0 * kPanel * (double)ncols * rows * batch;
+    const double bytes = (2.0 * r * ncols + rows * kPanel) * 4.0 * batch;
+    e = traced(QR_KERNEL_APPLY, flops, bytes, s, [&] {
+      return qr::launch_apply(H + (int64_t)J0 * ldh + J0, sHb, ldh, C + (int64_t)J0 * ldc + c0,
+                              sCb, ldc, nblk, r, ncols, Tw + (int64_t)q0 * kPanel * kPanel, sTw,
+                              trans, kv_last > kPanel ? kPanel : kv_last, batch, s);
+    });
+    if (e != hipSuccess) return to_status(e);
+  }
+  return QR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qr_ormqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int64_t sTaub,
+                 float* C, int64_t sCb, int64_t ldc, int n, int m, int trans, int batch,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0 || n < 0 || m < 0 || sHb < 0 || sTaub < 0 || sCb < 0) return QR_EINVAL;
+  if (trans != 0 && trans != 1) return QR_EINVAL;
+  if (batch == 0 || n == 0 || m == 0) return QR_OK;
+  if (!H || !tau || !C) return QR_EINVAL;
+  if (n > kMaxN) return QR_EUNSUPPORTED;
+  if (ldh < n || ldc < m || sTaub < n) return QR_EINVAL;
+  if (batch > 1 && (sHb < (int64_t)(n - 1) * ldh + n || sCb < (int64_t)(n - 1) * ldc + m))
+    return QR_EINVAL;
+  if (!workspace || workspace_bytes < qr_ormqr_f32_workspace(batch, n)) return QR_EWORKSPACE;
+  return apply_q(H, sHb, ldh, tau, sTaub, C, sCb, ldc, n, m, trans != 0, false, batch,
+                 static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+int qr_orgqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int64_t sTaub,
+                 float* Q, int64_t sQb, int64_t ldq, int n, int batch, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (batch < 0 || n < 0 || sHb < 0 || sTaub < 0 || sQb < 0) return QR_EINVAL;
+  if (batch == 0 || n == 0) return QR_OK;
+  if (!H || !tau || !Q) return QR_EINVAL;
+  if (n > kMaxN) return QR_EUNSUPPORTED;
+  if (ldh < n || ldq < n || sTaub < n) return QR_EINVAL;
+  if (batch > 1 && (sHb < (int64_t)(n - 1) * ldh + n || sQb < (int64_t)(n - 1) * ldq + n))
+    return QR_EINVAL;
+  if (overlaps(H, ((size_t)(batch - 1) * sHb + (size_t)(n - 1) * ldh + n) * sizeof(float), Q,
+               ((size_t)(batch - 1) * sQb + (size_t)(n - 1) * ldq + n) * sizeof(float)))
+    return QR_EINVAL;
+  if (!workspace || workspace_bytes < qr_ormqr_f32_workspace(batch, n)) return QR_EWORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = traced(QR_KERNEL_COPY, 0.0, (double)n * n * 4.0 * batch, s,
+                              [&] { return qr::launch_eye(Q, sQb, ldq, batch, n, s); });
+  if (e != hipSuccess) return to_status(e);
+  return apply_q(H, sHb, ldh, tau, sTaub, Q, sQb, ldq, n, n, false, true, batch,
+                 static_cast<float*>(workspace), s);
 }
 
 int qr_trace_enable(unsigned kernel_mask) {

@@ -77,11 +77,12 @@ __device__ __forceinline__ void wave_sync() {
 
 // Stage this wave's tiles [t0, t0 + kStageTiles) of V_q into vb (tile-local
 // index tt = t - t0): lane l copies row l/4, columns 4(l%4)..+3 of each tile.
-// Rows above V_q's diagonal are zero, the diagonal is 1, rows >= r are zero.
+// Rows above V_q's diagonal are zero, the diagonal is 1, rows >= r are zero;
+// columns >= kv (a block narrower than 16 at the matrix edge) are zero and not read.
 template <int NW, int RL>
 __device__ __forceinline__ void stage_v(float* __restrict__ vb, const float* __restrict__ Vq,
                                         int64_t ldh, int q16, int r, int t0, int w, int lane,
-                                        bool vec4) {
+                                        bool vec4, int kv) {
   constexpr int kStageTiles = StageTiles<NW, RL>::value;
   const int lr = lane >> 2, lc = 4 * (lane & 3);
 #pragma unroll
@@ -93,13 +94,11 @@ __device__ __forceinline__ void stage_v(float* __restrict__ vb, const float* __r
     f32x4 val = {0.0f, 0.0f, 0.0f, 0.0f};
     if (i >= 0 && r0 + lr < r) {
       const float* src = Vq + (int64_t)i * ldh + lc;
-      if (vec4) {
+      if (vec4 && lc + 4 <= kv) {
         val = *reinterpret_cast<const f32x4*>(src);
       } else {
-        val[0] = src[0];
-        val[1] = src[1];
-        val[2] = src[2];
-        val[3] = src[3];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = (lc + e < kv) ? src[e] : 0.0f;
       }
       if (i < 16) {  // diagonal tile: unit lower-triangular mask
 #pragma unroll
@@ -111,13 +110,14 @@ __device__ __forceinline__ void stage_v(float* __restrict__ vb, const float* __r
 }
 
 // c (a 16-column strip of r rows, strip layout) := (I - V T V^T)^T c for the
-// 16-wide reflector block V stored at Vq (its row 0 is strip row q16), T = Tq.
+// 16-wide reflector block V stored at Vq (its row 0 is strip row q16), T = Tq;
+// with kTransT = false, c := (I - V T V^T) c instead.
 // Three workgroup barriers; every thread of the workgroup must call it.
-template <int NW, int RL>
+template <int NW, int RL, bool kTransT = true>
 __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restrict__ Vq,
                                            int64_t ldh, int q16, int r,
                                            const float* __restrict__ Tq, WyShared<NW, RL>& sh,
-                                           int w, int lane) {
+                                           int w, int lane, int kv = 16) {
   using S = Strip<NW, RL>;
   constexpr int kStageTiles = StageTiles<NW, RL>::value;
   constexpr int kChunks = (S::kTiles + kStageTiles - 1) / kStageTiles;
@@ -130,7 +130,7 @@ __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restri
   f32x4 accw = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
-    stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4);
+    stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4, kv);
     wave_sync();
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
@@ -158,12 +158,17 @@ __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restri
   }
   __syncthreads();
   if (threadIdx.x < 256) {
-    // W2 = T^T W  (T upper triangular)
+    // W2 = T^T W, or T W (T upper triangular)
     const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
     float s = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
-      if (q <= i) s = fmaf(sh.ts[q][i], sh.wsum[q][j], s);
+    for (int q = 0; q < 16; ++q) {
+      if constexpr (kTransT) {
+        if (q <= i) s = fmaf(sh.ts[q][i], sh.wsum[q][j], s);
+      } else {
+        if (q >= i) s = fmaf(sh.ts[i][q], sh.wsum[q][j], s);
+      }
+    }
     sh.w2[i][j] = s;
   }
   __syncthreads();
@@ -177,7 +182,7 @@ __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restri
   for (int ch = kChunks - 1; ch >= 0; --ch) {
     if (ch != kChunks - 1) {
       wave_sync();
-      stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4);
+      stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4, kv);
       wave_sync();
     }
 #pragma unroll
@@ -514,6 +519,39 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   store_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
 }
 
+// Apply nblk 16-wide reflector blocks (V_q at V + 16 q (ldv + 1) of each matrix,
+// T_q at Tws + 256 q) to the 16-column strips of C (r rows, row stride ldc): C :=
+// Q^T C with blocks in order 0..nblk-1 (kTrans), or C := Q C with blocks in order
+// nblk-1..0, Q = (I - V_0 T_0 V_0^T) ... (I - V_{nblk-1} T_{nblk-1} V^T). 1-D grid
+// of nstrips * batch workgroups, XCD-aware like k_trail.
+template <int NW, int RL, bool kTrans>
+__global__ __launch_bounds__(64 * NW) void k_apply(const float* __restrict__ V, int64_t sVb,
+                                                   int64_t ldv, float* __restrict__ C,
+                                                   int64_t sCb, int64_t ldc, int nblk, int r,
+                                                   int ncols, const float* __restrict__ Tws,
+                                                   int64_t sTwb, int kv_last) {
+  __shared__ WyShared<NW, RL> wy;
+  const int nstrips = (ncols + 15) / 16;
+  const int id = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int b = id / nstrips;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const float* Vb = V + (int64_t)b * sVb;
+  const int s0 = 16 * (id - b * nstrips);
+  float* P = C + (int64_t)b * sCb + s0;
+  const float* Tb = Tws + (int64_t)b * sTwb;
+  const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
+
+  float c[RL];
+  load_strip<NW, RL>(c, P, ldc, r, ncol, w, lane);
+  for (int i = 0; i < nblk; ++i) {
+    const int q = kTrans ? i : nblk - 1 - i;
+    apply_wy16<NW, RL, kTrans>(c, Vb + (int64_t)(16 * q) * ldv + 16 * q, ldv, 16 * q, r,
+                               Tb + 256 * q, wy, w, lane, q == nblk - 1 ? kv_last : 16);
+  }
+  store_strip<NW, RL>(c, P, ldc, r, ncol, w, lane);
+}
+
 // (NW, RL) for r rows: 4 NW RL >= r and NW > p for every panel index used.
 #define QR_STRIP_DISPATCH(r, CASE)   \
   if ((r) <= 128) {                  \
@@ -581,6 +619,28 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
   QR_STRIP_DISPATCH(r, QR_TRAIL_CASE)
 #endif
 #undef QR_TRAIL_CASE
+  return hipGetLastError();
+}
+
+hipError_t launch_apply(const float* V, int64_t sVb, int64_t ldv, float* C, int64_t sCb,
+                        int64_t ldc, int nblk, int r, int ncols, const float* Tws, int64_t sTwb,
+                        bool trans, int kv_last, int batch, hipStream_t stream) {
+  if (ncols <= 0) return hipSuccess;
+  if (nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || kv_last < 1 || kv_last > 16 ||
+      r < 16 * (nblk - 1) + kv_last)
+    return hipErrorInvalidValue;
+  const int64_t wgs = (int64_t)((ncols + 15) / 16) * batch;
+  if (wgs > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)wgs);
+#define QR_APPLY_CASE(NWV, RLV)                                                                \
+  if (trans)                                                                                 \
+    hipLaunchKernelGGL((k_apply<NWV, RLV, true>), grid, dim3(64 * NWV), 0, stream, V, sVb, ldv, \
+                       C, sCb, ldc, nblk, r, ncols, Tws, sTwb, kv_last);                     \
+  else                                                                                       \
+    hipLaunchKernelGGL((k_apply<NWV, RLV, false>), grid, dim3(64 * NWV), 0, stream, V, sVb,   \
+                       ldv, C, sCb, ldc, nblk, r, ncols, Tws, sTwb, kv_last)
+  QR_STRIP_DISPATCH(r, QR_APPLY_CASE)
+#undef QR_APPLY_CASE
   return hipGetLastError();
 }
 

@@ -15,18 +15,23 @@ namespace qr {
 
 constexpr int kLarftMaxK = 64;
 
-__global__ __launch_bounds__(256) void k_larft(const float* __restrict__ V, int64_t sVb,
-                                               int64_t ldv, int m, int k,
-                                               const float* __restrict__ tau, int64_t sTaub,
-                                               float* __restrict__ T, int64_t sTb, int64_t ldt) {
-  __shared__ float vs[64][kLarftMaxK + 1];
-  __shared__ float S[kLarftMaxK][kLarftMaxK + 1];
-  __shared__ float Ts[kLarftMaxK][kLarftMaxK + 1];
-  __shared__ float taus[kLarftMaxK];
+struct LarftShared {
+  float vs[64][kLarftMaxK + 1];
+  float S[kLarftMaxK][kLarftMaxK + 1];
+  float Ts[kLarftMaxK][kLarftMaxK + 1];
+  float taus[kLarftMaxK];
+};
 
-  const int b = blockIdx.x;
+// T (k x k, row stride ldt) of the k reflectors stored below the diagonal of
+// the m x k block Vb, with coefficients taub[0..k-1]. One workgroup of 256.
+__device__ void larft_block(const float* __restrict__ Vb, int64_t ldv, int m, int k,
+                            const float* __restrict__ taub, float* __restrict__ Tb, int64_t ldt,
+                            LarftShared& sh) {
+  auto& vs = sh.vs;
+  auto& S = sh.S;
+  auto& Ts = sh.Ts;
+  auto& taus = sh.taus;
   const int tid = threadIdx.x;
-  const float* Vb = V + (int64_t)b * sVb;
   const int npairs = k * (k - 1) / 2;  // strictly upper (p < q)
   constexpr int kMaxPer = (kLarftMaxK * (kLarftMaxK - 1) / 2 + 255) / 256;
   float acc[kMaxPer];
@@ -72,7 +77,7 @@ __global__ __launch_bounds__(256) void k_larft(const float* __restrict__ V, int6
       S[pi - base][q] = acc[s];
     }
   }
-  if (tid < k) taus[tid] = tau[(int64_t)b * sTaub + tid];
+  if (tid < k) taus[tid] = taub[tid];
   for (int idx = tid; idx < k * k; idx += 256) Ts[idx / k][idx % k] = 0.0f;
   __syncthreads();
 
@@ -87,11 +92,38 @@ __global__ __launch_bounds__(256) void k_larft(const float* __restrict__ V, int6
     if (tid == i) Ts[i][i] = ti;
     __syncthreads();
   }
-  float* Tb = T + (int64_t)b * sTb;
   for (int idx = tid; idx < k * k; idx += 256) {
     const int p = idx / k, q = idx - (idx / k) * k;
     Tb[(int64_t)p * ldt + q] = Ts[p][q];
   }
+}
+
+__global__ __launch_bounds__(256) void k_larft(const float* __restrict__ V, int64_t sVb,
+                                               int64_t ldv, int m, int k,
+                                               const float* __restrict__ tau, int64_t sTaub,
+                                               float* __restrict__ T, int64_t sTb, int64_t ldt) {
+  __shared__ LarftShared sh;
+  const int b = blockIdx.x;
+  larft_block(V + (int64_t)b * sVb, ldv, m, k, tau + (int64_t)b * sTaub, T + (int64_t)b * sTb, ldt,
+              sh);
+}
+
+// T of every 16-wide panel of factored n x n matrices: workgroup (p, b) builds
+// the 16 x 16 T of panel p of matrix b (kw = min(16, n - 16 p) reflectors,
+// zero-padded to 16 x 16) at T + b sTb + 256 p.
+__global__ __launch_bounds__(256) void k_larft_panels(const float* __restrict__ H, int64_t sHb,
+                                                      int64_t ldh, int n,
+                                                      const float* __restrict__ tau,
+                                                      int64_t sTaub, float* __restrict__ T,
+                                                      int64_t sTb) {
+  __shared__ LarftShared sh;
+  const int p = blockIdx.x, b = blockIdx.y;
+  const int j0 = 16 * p, kw = min(16, n - j0);
+  float* Tb = T + (int64_t)b * sTb + 256 * p;
+  for (int idx = threadIdx.x; idx < 256; idx += 256) Tb[idx] = 0.0f;
+  __syncthreads();
+  larft_block(H + (int64_t)b * sHb + (int64_t)j0 * ldh + j0, ldh, n - j0, kw,
+              tau + (int64_t)b * sTaub + j0, Tb, 16, sh);
 }
 
 hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
@@ -100,6 +132,15 @@ hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, 
   if (k < 1 || k > kLarftMaxK || m < k) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_larft, dim3(batch), dim3(256), 0, stream, V, sVb, ldv, m, k, tau, sTaub, T,
                      sTb, ldt);
+  return hipGetLastError();
+}
+
+hipError_t launch_larft_panels(const float* H, int64_t sHb, int64_t ldh, int n, const float* tau,
+                               int64_t sTaub, float* T, int64_t sTb, int batch,
+                               hipStream_t stream) {
+  if (n < 1 || batch < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_larft_panels, dim3((n + 15) / 16, batch), dim3(256), 0, stream, H, sHb, ldh,
+                     n, tau, sTaub, T, sTb);
   return hipGetLastError();
 }
 

@@ -156,3 +156,59 @@ def wy_update(Hblk: torch.Tensor, T: torch.Tensor):
         )
     _lib.check("qr_wy_update_f32", st)
     return out
+
+
+def _ormqr_into(H: torch.Tensor, tau: torch.Tensor, C: torch.Tensor, trans: bool) -> None:
+    lib = _lib.load()
+    b, n, m = C.shape
+    need = int(lib.qr_ormqr_f32_workspace(b, n))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=C.device)
+    with torch.cuda.device(C.device):
+        st = lib.qr_ormqr_f32(
+            H.data_ptr(), H.stride(0), H.stride(1), tau.data_ptr(), tau.stride(0), C.data_ptr(),
+            C.stride(0), C.stride(1), n, m, int(trans), b, ws.data_ptr(), need,
+            _stream(C.device),
+        )
+    _lib.check("qr_ormqr_f32", st)
+
+
+def _check_factors(H: torch.Tensor, tau: torch.Tensor) -> None:
+    _check_input(H)
+    b, n, _ = H.shape
+    if tau.shape != (b, n) or tau.dtype != torch.float32 or tau.device != H.device:
+        raise ValueError(f"tau must be float32 ({b}, {n}) on {H.device}")
+
+
+def ormqr(H: torch.Tensor, tau: torch.Tensor, C: torch.Tensor, transpose: bool = False):
+    """``Q^T C`` (``transpose=True``) or ``Q C`` for the Q of ``(H, tau)`` from
+    :func:`geqrf`; ``C`` is ``(batch, n, m)`` and is not modified (LAPACK sormqr,
+    side 'L')."""
+    _check_factors(H, tau)
+    b, n, _ = H.shape
+    if C.dim() != 3 or C.shape[:2] != (b, n) or C.dtype != torch.float32 or C.device != H.device:
+        raise ValueError(f"C must be float32 ({b}, {n}, m) on {H.device}")
+    out = C.contiguous().clone()
+    if out.numel():
+        _ormqr_into(H.contiguous(), tau.contiguous(), out, transpose)
+    return out
+
+
+def orgqr(H: torch.Tensor, tau: torch.Tensor) -> torch.Tensor:
+    """Q (batch, n, n) of ``(H, tau)`` from :func:`geqrf`, like
+    ``torch.linalg.householder_product(H, tau)`` (LAPACK sorgqr)."""
+    _check_factors(H, tau)
+    lib = _lib.load()
+    b, n, _ = H.shape
+    Hc, tc = H.contiguous(), tau.contiguous()
+    Q = torch.empty((b, n, n), dtype=torch.float32, device=H.device)
+    if Q.numel() == 0:
+        return Q
+    need = int(lib.qr_ormqr_f32_workspace(b, n))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=H.device)
+    with torch.cuda.device(H.device):
+        st = lib.qr_orgqr_f32(
+            Hc.data_ptr(), Hc.stride(0), Hc.stride(1), tc.data_ptr(), tc.stride(0), Q.data_ptr(),
+            Q.stride(0), Q.stride(1), n, b, ws.data_ptr(), need, _stream(H.device),
+        )
+    _lib.check("qr_orgqr_f32", st)
+    return Q

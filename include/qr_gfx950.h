@@ -37,7 +37,8 @@ typedef enum qr_kernel_id {
   QR_KERNEL_PANEL = 1,  /* kernel (b), incl. its left-looking block update */
   QR_KERNEL_TRAIL = 2,  /* kernel (d), trailing compact-WY update */
   QR_KERNEL_COPY = 3,   /* strided A -> H copy */
-  QR_KERNEL_LARFT = 4   /* kernel (c) */
+  QR_KERNEL_LARFT = 4,  /* kernel (c) */
+  QR_KERNEL_APPLY = 5   /* block-reflector application of orgqr / ormqr */
 } qr_kernel_id;
 
 /* Human-readable text for a qr_status value (static storage). */
@@ -104,6 +105,35 @@ int qr_larft_f32(const float* V, int64_t sVb, int64_t ldv, int m, int k, const f
  */
 int qr_wy_update_f32(float* H, int64_t sHb, int64_t ldh, int j0, int nblk, int r, int c,
                      const float* T, int64_t sTb, int batch, void* stream);
+
+/*
+ * Bytes of device workspace qr_ormqr_f32 / qr_orgqr_f32 need for (batch, n):
+ * the 16 x 16 T of every 16-wide panel.
+ */
+size_t qr_ormqr_f32_workspace(int batch, int n);
+
+/*
+ * Apply Q of a factorisation (H, tau) from qr_geqrf_f32 (n x n, row stride ldh)
+ * to C (n x m, row stride ldc) in place: trans = 1 gives C := Q^T C, trans = 0
+ * gives C := Q C, with Q = H_0 H_1 ... H_{n-1} (LAPACK sormqr, side = 'L').
+ * T of each panel is rebuilt from (H, tau) (larft), then the 16-wide block
+ * reflectors are applied with FP32 MFMA. No counterpart kernel in the
+ * reference: its consumers of (H, tau) call torch's householder_product and
+ * matmul (src/qrbench/checker.py:129-158).
+ */
+int qr_ormqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int64_t sTaub,
+                 float* C, int64_t sCb, int64_t ldc, int n, int m, int trans, int batch,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Form Q (n x n, row stride ldq; must not overlap H) of a factorisation
+ * (H, tau): Q := Q I (LAPACK sorgqr). Replaces
+ * torch.linalg.householder_product(H, tau) as used by the reference's gates
+ * (src/qrbench/checker.py:129).
+ */
+int qr_orgqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int64_t sTaub,
+                 float* Q, int64_t sQb, int64_t ldq, int n, int batch, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /*
  * Launch tracer (measurement only; no counterpart in the reference, whose

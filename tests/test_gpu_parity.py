@@ -337,6 +337,64 @@ def test_tau_range_and_zero_columns(n):
     assert nz.numel() == tau.numel() - 7
 
 
+EPS32 = 2.0**-23
+
+
+@pytest.mark.parametrize("n,batch", [(16, 3), (40, 2), (64, 3), (100, 2), (200, 2), (513, 2)])
+def test_orgqr_matches_householder_product(n, batch):
+    # Q from (H, tau) is backward stable whatever A's conditioning: compare with
+    # fp64 householder_product of the same factors, elementwise, and check
+    # orthogonality and Q R = A.
+    _say(f"orgqr n={n}")
+    A = _gauss(batch, n, seed=3 * n + 1).to(DEV)
+    H, tau = hip_qr.geqrf(A)
+    Q = hip_qr.orgqr(H, tau)
+    torch.cuda.synchronize()
+    Q64 = torch.linalg.householder_product(H.double().cpu(), tau.double().cpu())
+    err = (Q.double().cpu() - Q64).abs().max().item()
+    assert err <= 4 * n * EPS32, err
+    I = torch.eye(n, dtype=torch.float64)
+    orth = (Q64.transpose(1, 2) @ Q.double().cpu() - I).abs().max().item()
+    assert orth <= 100 * n * EPS32, orth
+    R = torch.triu(H.double().cpu())
+    resid = (Q.double().cpu() @ R - A.double().cpu()).abs().max().item()
+    assert resid <= 20 * n * EPS32 * A.abs().max().item() * n ** 0.5, resid
+
+
+@pytest.mark.parametrize("n,m,batch", [(64, 24, 2), (100, 37, 2), (200, 16, 1), (513, 70, 2)])
+def test_ormqr_both_sides_and_round_trip(n, m, batch):
+    _say(f"ormqr n={n} m={m}")
+    A = _gauss(batch, n, seed=n + m).to(DEV)
+    H, tau = hip_qr.geqrf(A)
+    g = torch.Generator().manual_seed(m)
+    C = torch.randn(batch, n, m, generator=g).to(DEV)
+    QtC = hip_qr.ormqr(H, tau, C, transpose=True)
+    QC = hip_qr.ormqr(H, tau, C, transpose=False)
+    back = hip_qr.ormqr(H, tau, QtC, transpose=False)
+    torch.cuda.synchronize()
+    Q64 = torch.linalg.householder_product(H.double().cpu(), tau.double().cpu())
+    C64 = C.double().cpu()
+    scale = C64.abs().max().item() * n ** 0.5
+    tol = 4 * n * EPS32 * scale
+    assert (QtC.double().cpu() - Q64.transpose(1, 2) @ C64).abs().max().item() <= tol
+    assert (QC.double().cpu() - Q64 @ C64).abs().max().item() <= tol
+    assert (back.double().cpu() - C64).abs().max().item() <= 2 * tol
+    # Q^T A is R: zero below the diagonal, triu(H) on and above it.
+    QtA = hip_qr.ormqr(H, tau, A, transpose=True).double().cpu()
+    R = torch.triu(H.double().cpu())
+    assert (QtA - R).abs().max().item() <= 20 * n * EPS32 * A.abs().max().item() * n ** 0.5
+
+
+def test_orgqr_on_smalln_and_official_b20_n32():
+    _say("orgqr on fused small-n factors")
+    prob = inputs.make_benchmark_problem(inputs.BENCHMARK_SHAPES[0], seed=11, device="cpu")
+    A = prob.tensor.to(DEV)
+    H, tau = hip_qr.geqrf(A)
+    Q = hip_qr.orgqr(H, tau)
+    Q64 = torch.linalg.householder_product(H.double().cpu(), tau.double().cpu())
+    assert (Q.double().cpu() - Q64).abs().max().item() <= 4 * 32 * EPS32
+
+
 def test_variant_registry_runs_hip_path():
     from gpumode_qr_amd.variants import CHAMPION, VARIANTS
 

@@ -85,3 +85,17 @@ def test_argument_validation_without_launch(lib):
     assert lib.qr_larft_f32(h, 100, 70, 100, 70, t, 70, t, 4900, 70, 1, None) == 2
     assert lib.qr_wy_update_f32(h, 1000, 50, 0, 9, 200, 4, t, 4096, 1, None) == 1  # nblk > 8
     assert lib.qr_wy_update_f32(h, 1000, 50, 0, 2, 5000, 4, t, 512, 1, None) == 2  # r > 4096
+    # orgqr / ormqr
+    assert lib.qr_ormqr_f32_workspace(2, 100) >= 2 * 7 * 256 * 4  # one 16 x 16 T per panel
+    assert lib.qr_ormqr_f32_workspace(0, 100) == 0
+    assert lib.qr_ormqr_f32(h, 10000, 100, t, 100, p, 10000, 100, 100, 100, 2, 1, h, 1 << 20,
+                            None) == 1  # trans not 0/1
+    assert lib.qr_ormqr_f32(h, 10000, 100, t, 100, p, 10000, 100, 100, 100, 1, 1, None, 0,
+                            None) == 3  # no workspace
+    assert lib.qr_ormqr_f32(h, 10000, 50, t, 100, p, 10000, 100, 100, 100, 1, 1, h, 1 << 20,
+                            None) == 1  # ldh < n
+    assert lib.qr_ormqr_f32(h, 1, 5000, t, 5000, p, 1, 5000, 5000, 8, 1, 1, h, 1 << 30,
+                            None) == 2  # n > 4096
+    assert lib.qr_ormqr_f32(h, 0, 0, t, 0, p, 0, 0, 0, 8, 1, 1, None, 0, None) == 0  # n = 0
+    assert lib.qr_orgqr_f32(h, 10000, 100, t, 100, h, 10000, 100, 100, 1, h, 1 << 20,
+                            None) == 1  # Q overlaps H
