@@ -41,8 +41,10 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 METRIC = "geomean median ms (cfg 2-5); GFLOP/s (4/3·n³·b) & % MI355X FP32 peak"
 
-# Matrices per config factored by the CPU baseline (bounded sample).
-CPU_SAMPLE = {1: 64, 2: 256, 3: 16, 4: 4, 5: 1}
+# Matrices per config factored by the CPU baseline: the full batches (about
+# 1.6 s per repetition on 16 host threads), median of CPU_REPS repetitions.
+CPU_SAMPLE = {1: 64, 2: 2048, 3: 640, 4: 64, 5: 16}
+CPU_REPS = 5
 
 # Published MI350X medians of the reference's Triton champion at the nearest
 # shapes (cfg 2's stand-in is b256 n64): db/20260708T044736Z_hh_panel_tuned.json:169,
@@ -174,7 +176,7 @@ def cpu_baseline(cfgs: list[int], torch) -> dict:
         sample = A[:k].contiguous()
         torch.geqrf(sample)  # warm-up
         reps = []
-        for _ in range(3):
+        for _ in range(CPU_REPS):
             t0 = time.perf_counter()
             torch.geqrf(sample)
             reps.append(time.perf_counter() - t0)
@@ -193,7 +195,7 @@ def cpu_baseline(cfgs: list[int], torch) -> dict:
         "sample": "torch.geqrf (LAPACK sgeqrf, the reference's torch_geqrf baseline) on the CPU, "
                   + ", ".join(f"cfg{c}: {v['sample_matrices']} matrices"
                               for c, v in per_cfg.items())
-                  + "; median of 3, scaled linearly to the full batch",
+                  + f"; median of {CPU_REPS} repetitions, scaled linearly to the full batch",
         "per_config": per_cfg,
     }
 
