@@ -269,43 +269,114 @@ __device__ __forceinline__ void publish_x(float* __restrict__ xw, const float (&
   }
 }
 
-// Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
-// Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
-// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p.
+// Shared memory of k_panel.
 template <int NW, int RL>
-__global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
-                                                   int64_t ldh, int J0, int p, int r, int kw,
-                                                   float* __restrict__ tau, int64_t sTaub,
-                                                   float* __restrict__ Tws, int64_t sTwb) {
-  using S = Strip<NW, RL>;
-  __shared__ WyShared<NW, RL> wy;
-  __shared__ __align__(16) float xs[NW][4 * RL];
+struct PanelShared {
+  WyShared<NW, RL> wy;
+  alignas(16) float xs[NW][4 * RL];  // per-wave x slab of the general pass
   // Row stride 4 NW + 4: the b128 reads of 16 columns land on distinct banks.
-  __shared__ __align__(16) float red[2][16][4 * NW + 4];
-  __shared__ float erow[2][16];
-  __shared__ __align__(16) float zbuf[16][16];
-  __shared__ float tbuf[16][17];
-  __shared__ float taus[16];
-  __shared__ float scr[2][NW];
+  alignas(16) float red[2][16][4 * NW + 4];
+  float erow[2][16];
+  alignas(16) float zbuf[16][16];
+  float taus[16];
+  float scr[2][NW];
+};
 
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+// What lane k keeps of column k's own step.
+struct PanelCol {
+  float beta = 0.0f, gamma = 1.0f, pre = 1.0f, tau = 0.0f;
+};
+
+// x^T c_k summed over the 4 NW partials (wave w, row group g) at rp.
+template <int NW>
+__device__ __forceinline__ float panel_dot_sum(const float* __restrict__ rp) {
+  f32x4 a4 = *reinterpret_cast<const f32x4*>(rp);
+#pragma unroll
+  for (int u = 1; u < NW; ++u) {
+    const f32x4 q4 = *reinterpret_cast<const f32x4*>(rp + 4 * u);
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) a4[e4] += q4[e4];
+  }
+  return (a4[0] + a4[1]) + (a4[2] + a4[3]);
+}
+
+// Fast pass over the kw column steps of the panel whose diagonal rows
+// 16p..16p+15 are tile 0 of wave p. The steps are unrolled, and x (column J
+// below the diagonal) is read straight from the registers of lane J of each
+// 16-lane row by DPP row_newbcast, folded into the v_fmac of the dot and of
+// the update: no LDS traffic for x and one workgroup barrier per step.
+// Returns false, with c and st meaningless, if some column was outside the
+// fast reflector's range (zero, tiny or huge norm); the result is then to be
+// recomputed by panel_general_pass.
+template <int NW, int RL>
+__device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, RL>& sh, int p,
+                                                int r, int kw, int w, int lane, PanelCol& st) {
+  using S = Strip<NW, RL>;
   const int k = lane & 15, g = lane >> 4;
-  float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
-  float* P = Blk + 16 * p;
-  float* Tb = Tws + (int64_t)b * sTwb;
-
-  float c[RL];
-  load_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
-  for (int q = 0; q < p; ++q)
-    apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q, wy,
-                       w, lane);
-
-  // The diagonal rows 16p..16p+15 are tile 0 of wave p (NW > p is required).
   const int d0 = 16 * p;
-  float my_beta = 0.0f, my_gamma = 1.0f, my_pre = 1.0f, my_tau = 0.0f;
-  float* xw = xs[w];
+  bool ok = true;
+  static_for<0, 16>([&](auto jc) __attribute__((always_inline)) {
+    constexpr int J = decltype(jc)::value;
+    if (J >= kw) return;
+    const int dj = d0 + J;
+    if (w == p && g == (J >> 2)) sh.erow[J & 1][k] = c[J & 3];
+    // Rows <= dj (where x is zero) all lie in tile 0.
+    float dv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float xb = row_bcast16<J>(c[v]);
+      dv[v] = ((S::row(0, v, w, g) > dj) ? xb : 0.0f) * c[v];
+    }
+#pragma unroll
+    for (int t = 1; t < S::kTiles; ++t)
+      dot4_bcast16<J>(dv[0], dv[1], dv[2], dv[3], c[4 * t], c[4 * t + 1], c[4 * t + 2],
+                      c[4 * t + 3]);
+    sh.red[J & 1][k][4 * w + g] = (dv[0] + dv[1]) + (dv[2] + dv[3]);
+    __syncthreads();
+    const float ds = panel_dot_sum<NW>(sh.red[J & 1][k]);
+    const float e = sh.erow[J & 1][k];
+    const float sigma = readlane_f(ds, J);
+    const float alpha = readlane_f(e, J);
+    const bool ident = dj >= r - 1;  // no rows below the diagonal
+    ok = ok && (ident || reflector_fast_ok(alpha, sigma));
+    Reflector R = reflector_fast(alpha, sigma);
+    if (ident) R = reflector_identity(alpha);
+    const float wk = fmaf(R.gamma, ds, e);  // v_J^T c_k
+    const float cc = R.tau * wk;
+    const bool upd = (k > J) && (k < kw);
+    const float ncx = upd ? -(cc * R.gamma) : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float xb = row_bcast16<J>(c[v]);
+      c[v] = fmaf(ncx, (S::row(0, v, w, g) > dj) ? xb : 0.0f, c[v]);
+    }
+#pragma unroll
+    for (int t = 1; t < S::kTiles; ++t)
+      axpy4_bcast16<J>(c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3], ncx);
+    if (upd && w == p && g == (J >> 2)) c[J & 3] -= cc;  // v_J[dj] = 1
+    // Column J of T needs z_k = V_k^T v_J = (c_k[dj] + gamma x^T c_k) gamma_k, k < J.
+    if (w == 0 && g == 0 && k < J) sh.zbuf[J][k] = wk * st.gamma;
+    if (k == J) {
+      st.beta = R.beta;
+      st.gamma = R.gamma;
+      st.pre = 1.0f;
+      st.tau = R.tau;
+    }
+  });
+  return ok;
+}
+
+// General pass: the same steps for any column (slarfg's zero-norm and
+// rescaled branches included), a runtime loop with x published by the lanes of
+// column j into the wave's LDS slab.
+template <int NW, int RL>
+__device__ __forceinline__ void panel_general_pass(float (&c)[RL], PanelShared<NW, RL>& sh, int p,
+                                                   int r, int kw, int w, int lane,
+                                                   PanelCol& st) {
+  using S = Strip<NW, RL>;
+  const int k = lane & 15, g = lane >> 4;
+  const int d0 = 16 * p;
+  float* xw = sh.xs[w];
   // Small strips keep x in registers between the dot and the update.
   constexpr bool kKeepX = RL <= 32;
   constexpr int RX = kKeepX ? RL : 1;
@@ -316,8 +387,12 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   for (int j = 0; j < kw; ++j) {
     const int dj = d0 + j;
     if (w == p && g == (j >> 2)) {
+      // Opaque copies: a select between loads of c[0..3] would be folded into
+      // one load at a computed index, and c would no longer fit in registers.
+      float t0 = c[0], t1 = c[1], t2 = c[2], t3 = c[3];
+      asm("" : "+v"(t0), "+v"(t1), "+v"(t2), "+v"(t3));
       const int v = j & 3;
-      erow[j & 1][k] = (v == 0) ? c[0] : (v == 1) ? c[1] : (v == 2) ? c[2] : c[3];
+      sh.erow[j & 1][k] = (v == 0) ? t0 : (v == 1) ? t1 : (v == 2) ? t2 : t3;
     }
     wave_sync();
     float x[RX];
@@ -332,21 +407,10 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       }
     }
     // Partial dot of (wave w, row group g) for column k, summed after the barrier.
-    red[j & 1][k][4 * w + g] = (dv[0] + dv[1]) + (dv[2] + dv[3]);
+    sh.red[j & 1][k][4 * w + g] = (dv[0] + dv[1]) + (dv[2] + dv[3]);
     __syncthreads();
-    float ds;
-    {
-      const float* rp = red[j & 1][k];
-      f32x4 a4 = *reinterpret_cast<const f32x4*>(rp);
-#pragma unroll
-      for (int u = 1; u < NW; ++u) {
-        const f32x4 q4 = *reinterpret_cast<const f32x4*>(rp + 4 * u);
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) a4[e4] += q4[e4];
-      }
-      ds = (a4[0] + a4[1]) + (a4[2] + a4[3]);
-    }
-    const float e = erow[j & 1][k];
+    const float ds = panel_dot_sum<NW>(sh.red[j & 1][k]);
+    const float e = sh.erow[j & 1][k];
     const float sigma = readlane_f(ds, j);
     const float alpha = readlane_f(e, j);
 
@@ -357,17 +421,17 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
     } else if (reflector_fast_ok(alpha, sigma)) {
       R = reflector_fast(alpha, sigma);
     } else {
-      // Rare path (zero, tiny or huge column): scaled norm of x from the slab,
-      // two workgroup reductions.
+      // Zero, tiny or huge column: scaled norm of x from the slab, two
+      // workgroup reductions.
       float xm = 0.0f;
       for (int idx = lane; idx < 4 * RL; idx += 64) xm = fmaxf(xm, fabsf(xw[idx]));
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) xm = fmaxf(xm, __shfl_xor(xm, o));
-      if (lane == 0) scr[0][w] = xm;
+      if (lane == 0) sh.scr[0][w] = xm;
       __syncthreads();
       float xmax = 0.0f;
 #pragma unroll
-      for (int u = 0; u < NW; ++u) xmax = fmaxf(xmax, scr[0][u]);
+      for (int u = 0; u < NW; ++u) xmax = fmaxf(xmax, sh.scr[0][u]);
       float sq = 0.0f;
       if (xmax > 0.0f) {
         for (int idx = lane; idx < 4 * RL; idx += 64) {
@@ -377,11 +441,11 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       }
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) sq += __shfl_xor(sq, o);
-      if (lane == 0) scr[1][w] = sq;
+      if (lane == 0) sh.scr[1][w] = sq;
       __syncthreads();
       float ssq = 0.0f;
 #pragma unroll
-      for (int u = 0; u < NW; ++u) ssq += scr[1][u];
+      for (int u = 0; u < NW; ++u) ssq += sh.scr[1][u];
       R = reflector_scaled(alpha, xmax, ssq);
       fast = false;
     }
@@ -407,35 +471,88 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
           }
         }
       }
-      if (upd && own_row) {
-        const int v = j & 3;
-        if (v == 0) c[0] -= cc;
-        else if (v == 1) c[1] -= cc;
-        else if (v == 2) c[2] -= cc;
-        else c[3] -= cc;
-      }
+      // v_j[dj] = 1 (unconditional stores at fixed indices, for the same reason)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) c[v] -= (upd && own_row && v == (j & 3)) ? cc : 0.0f;
     }
     // Column j of T needs z_k = V_k^T v_j = ((c_k[j] + (x^T c_k pre) gamma) pre_k)
     // gamma_k for k < j; pre gamma itself can overflow for tiny columns.
     if (w == 0 && g == 0 && k < j)
-      zbuf[j][k] = (fmaf(R.gamma, R.pre * ds, e) * my_pre) * my_gamma;
+      sh.zbuf[j][k] = (fmaf(R.gamma, R.pre * ds, e) * st.pre) * st.gamma;
     if (k == j) {
-      my_beta = R.beta;
-      my_gamma = R.gamma;
-      my_pre = R.pre;
-      my_tau = R.tau;
+      st.beta = R.beta;
+      st.gamma = R.gamma;
+      st.pre = R.pre;
+      st.tau = R.tau;
     }
     // x for step j+1 (every lane of this wave has finished reading the slab).
     if (j + 1 < kw) publish_x<NW, RL>(xw, c, dj + 1, k == j + 1, w, g);
   }
-  if (w == 0 && g == 0) taus[k] = (k < kw) ? my_tau : 0.0f;
+}
+
+// c := panel p (kw columns at Blk + 16 p, r rows, strip layout) after the
+// left-looking update with panels 0..p-1 of the outer block at Blk.
+template <int NW, int RL>
+__device__ __forceinline__ void panel_load_apply(float (&c)[RL], const float* __restrict__ Blk,
+                                                 int64_t ldh, int p, int r, int kw,
+                                                 const float* __restrict__ Tb,
+                                                 WyShared<NW, RL>& wy, int w, int lane) {
+  load_strip<NW, RL>(c, Blk + 16 * p, ldh, r, kw, w, lane);
+  for (int q = 0; q < p; ++q)
+    apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q,
+                       wy, w, lane);
+}
+
+// The fast pass can be switched off (every panel then takes the general pass).
+#ifndef QR_PANEL_FAST
+#define QR_PANEL_FAST 1
+#endif
+constexpr bool kPanelFastPass = QR_PANEL_FAST != 0;
+
+// Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
+// Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
+// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p.
+template <int NW, int RL>
+__global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
+                                                   int64_t ldh, int J0, int p, int r, int kw,
+                                                   float* __restrict__ tau, int64_t sTaub,
+                                                   float* __restrict__ Tws, int64_t sTwb) {
+  using S = Strip<NW, RL>;
+  __shared__ PanelShared<NW, RL> sh;
+
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int k = lane & 15, g = lane >> 4;
+  float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
+  float* P = Blk + 16 * p;
+  float* Tb = Tws + (int64_t)b * sTwb;
+
+  // The panel after the left-looking update with panels 0..p-1; the panel in
+  // HBM is not written before the end, so the general pass can start over.
+  float c[RL];
+  panel_load_apply<NW, RL>(c, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
+
+  PanelCol st;
+  bool ok = false;
+  if constexpr (kPanelFastPass) ok = panel_fast_pass<NW, RL>(c, sh, p, r, kw, w, lane, st);
+  if (!ok) [[unlikely]] {
+    if constexpr (kPanelFastPass) {
+      __syncthreads();  // every wave is past its last read of erow / red
+      panel_load_apply<NW, RL>(c, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
+      st = PanelCol{};
+    }
+    panel_general_pass<NW, RL>(c, sh, p, r, kw, w, lane, st);
+  }
+  const int d0 = 16 * p;
+  if (w == 0 && g == 0) sh.taus[k] = (k < kw) ? st.tau : 0.0f;
   __syncthreads();
 
   // T_p (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
   // Lane k of wave 0 holds row k of T in registers; z_j rows are b128 reads.
   if (w == 0 && g == 0) {
     float trow[16];
-    const float tk = taus[k];
+    const float tk = sh.taus[k];
 #pragma unroll
     for (int q = 0; q < 16; ++q) trow[q] = (q == k) ? tk : 0.0f;
 #pragma unroll
@@ -443,7 +560,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
       float z[16];
 #pragma unroll
       for (int q4 = 0; q4 < (j + 3) / 4; ++q4) {
-        const f32x4 zz = *reinterpret_cast<const f32x4*>(&zbuf[j][4 * q4]);
+        const f32x4 zz = *reinterpret_cast<const f32x4*>(&sh.zbuf[j][4 * q4]);
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) z[4 * q4 + e4] = zz[e4];
       }
@@ -453,14 +570,14 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
         if (q & 1) sb = fmaf(trow[q], z[q], sb);
         else sa = fmaf(trow[q], z[q], sa);
       }
-      const float tj = taus[j];
+      const float tj = sh.taus[j];
       // zbuf rows j >= kw are not written by this launch: never read them.
       trow[j] = (j < kw && k < j) ? -tj * (sa + sb) : trow[j];
     }
     float* Tp = Tb + 256 * p;
 #pragma unroll
     for (int q = 0; q < 16; ++q) Tp[k * 16 + q] = trow[q];
-    if (k < kw) tau[(int64_t)b * sTaub + J0 + d0 + k] = my_tau;
+    if (k < kw) tau[(int64_t)b * sTaub + J0 + d0 + k] = st.tau;
   }
 
   // Write back: R above the diagonal, beta on it, v = (x pre) gamma below.
@@ -471,7 +588,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
     for (int v = 0; v < 4; ++v) {
       const int row = S::row(t, v, w, g);
       c[4 * t + v] =
-          (row < kd) ? c[4 * t + v] : ((row == kd) ? my_beta : (c[4 * t + v] * my_pre) * my_gamma);
+          (row < kd) ? c[4 * t + v] : ((row == kd) ? st.beta : (c[4 * t + v] * st.pre) * st.gamma);
     }
   store_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
 }

@@ -151,6 +151,39 @@ __device__ __forceinline__ float row_bcast16_nocse(float v) {
   return out;
 }
 
+// a_v += x_v[J] * x_v for v < 4, where x_v[J] is x_v in lane J of the lane's
+// 16-lane row (DPP row_newbcast folded into v_fmac_f32, which the compiler does
+// not form by itself). The leading s_nop 4 gives the wait states a DPP source
+// needs after a VALU write of that register or of EXEC; the compiler's hazard
+// tracking does not look inside inline asm.
+template <int J>
+__device__ __forceinline__ void dot4_bcast16(float& a0, float& a1, float& a2, float& a3, float x0,
+                                             float x1, float x2, float x3) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  asm("s_nop 4\n\t"
+      "v_fmac_f32_dpp %0, %4, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %5, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %2, %6, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %3, %7, %7 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)
+      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J));
+}
+
+// x_v += x_v[J] * s for v < 4 (same broadcast and wait states as dot4_bcast16).
+// Each instruction reads its DPP source before writing it, and no instruction
+// reads a register written by the one before it.
+template <int J>
+__device__ __forceinline__ void axpy4_bcast16(float& x0, float& x1, float& x2, float& x3, float s) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  asm("s_nop 4\n\t"
+      "v_fmac_f32_dpp %0, %0, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %1, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %2, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %3, %3, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+      : "v"(s), "i"(J));
+}
+
 // Sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
 __device__ __forceinline__ float sum_over_rows16(float v) {
   v += __shfl_xor(v, 16);
