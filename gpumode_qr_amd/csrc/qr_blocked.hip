@@ -35,10 +35,8 @@ struct Strip {
   __device__ static __forceinline__ int tile_row0(int t, int w) { return 16 * (t * NW + w); }
 };
 
-// LDS of apply_wy16: each wave stages its own rows of V_q (up to kStageTiles
-// 16-row tiles at a time, row stride 20 floats: conflict-free for both the
-// b32 reads of the W phase and the b128 reads of the update phase), plus the
-// cross-wave reduction of W and the 16 x 16 T and W2.
+// Row stride (floats) of the V tiles staged in LDS: 20 keeps both the b32 reads
+// of the W phase and the b128 reads of the update phase free of bank conflicts.
 constexpr int kVStride = 20;
 
 // 16-row tiles of V staged per wave at a time (LDS budget: NW * tiles * 1.25 KB).
@@ -51,14 +49,6 @@ struct StageTiles {
   static constexpr int value = (RL / 4) < kMax ? (RL / 4) : kMax;
 };
 
-template <int NW, int RL>
-struct WyShared {
-  float vbuf[NW][StageTiles<NW, RL>::value * 16 * kVStride];
-  float red[NW][16][17];
-  float wsum[16][17];
-  float w2[16][17];
-  float ts[16][17];
-};
 
 // Element (i, col) of the unit lower-trapezoidal block V stored in place at P
 // with rows 0..rv-1; i may be negative (rows above the block are zero).
@@ -75,115 +65,172 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Stage this wave's tiles [t0, t0 + kStageTiles) of V_q into vb (tile-local
-// index tt = t - t0): lane l copies row l/4, columns 4(l%4)..+3 of each tile.
-// Rows above V_q's diagonal are zero, the diagonal is 1, rows >= r are zero;
-// columns >= kv (a block narrower than 16 at the matrix edge) are zero and not read.
+// ---------------------------------------------------------------------------
+// Compact-WY application of a sequence of 16-wide reflector blocks to a strip.
+//
+// * Each wave stages its own rows of V_q through LDS in chunks of kStageTiles
+//   16-row tiles (row stride kVStride): the W phase reads them as b32 in the
+//   A-operand layout, the update phase as b128 rows. Each chunk is loaded
+//   from HBM into registers (VChunk) one stage ahead: the loads of the next
+//   chunk, and at the end of a block those of the next block's first chunk, are
+//   in flight while the MFMAs of the current chunk run.
+// * The cross-wave reduction of W = V^T c takes two workgroup barriers: every
+//   wave writes its 16 x 16 partial as one b128 per lane (the MFMA accumulator
+//   layout, which is also the B-operand layout with K order {v, v+4, v+8,
+//   v+12}), 256 threads sum them, and every wave forms W2 = T^T W (or T W)
+//   from the sum with four MFMAs whose accumulator is exactly the operand of
+//   the update. No barrier is needed after the update: a wave writes the next
+//   partial only after the second barrier, when the sums have been read, and
+//   the next sum only after the next first barrier, when every wave has read W.
+// ---------------------------------------------------------------------------
+
+// This wave's part of one V chunk, in registers: lane l holds row l/4, columns
+// 4(l%4)..+3 of each of the chunk's tiles.
 template <int NW, int RL>
-__device__ __forceinline__ void stage_v(float* __restrict__ vb, const float* __restrict__ Vq,
-                                        int64_t ldh, int q16, int r, int t0, int w, int lane,
-                                        bool vec4, int kv) {
+struct VChunk {
+  f32x4 t[StageTiles<NW, RL>::value];
+};
+
+// A reflector block: V_q at Vq (its row 0 is strip row q16), kv columns.
+struct VBlock {
+  const float* V;
+  int q16;
+  int kv;
+};
+
+// LDS of apply_wy16p: per-wave V chunks, the NW partial W's and their sum.
+template <int NW, int RL>
+struct WyPipeShared {
+  float vbuf[NW][StageTiles<NW, RL>::value * 16 * kVStride];
+  alignas(16) float red[NW][64 * 4];
+  alignas(16) float wsum[64 * 4];
+};
+
+// Global loads of this wave's tiles [t0, t0 + kStageTiles) of block B: rows
+// above V's diagonal and rows >= r are zero, the diagonal is 1, columns >= kv
+// (a block narrower than 16 at the matrix edge) are zero and not read.
+template <int NW, int RL>
+__device__ __forceinline__ void load_v_chunk(VChunk<NW, RL>& ck, const VBlock& B, int64_t ldh,
+                                             int r, int t0, int w, int lane) {
   constexpr int kStageTiles = StageTiles<NW, RL>::value;
   const int lr = lane >> 2, lc = 4 * (lane & 3);
+  const bool vec4 = ((ldh & 3) == 0) && ((reinterpret_cast<uintptr_t>(B.V) & 15) == 0);
 #pragma unroll
   for (int tt = 0; tt < kStageTiles; ++tt) {
     const int t = t0 + tt;
-    if (t >= RL / 4) break;  // compile-time
-    const int r0 = 16 * (t * NW + w);
-    const int i = r0 + lr - q16;  // row within V_q
     f32x4 val = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (i >= 0 && r0 + lr < r) {
-      const float* src = Vq + (int64_t)i * ldh + lc;
-      if (vec4 && lc + 4 <= kv) {
-        val = *reinterpret_cast<const f32x4*>(src);
-      } else {
+    if (t < RL / 4) {
+      const int r0 = 16 * (t * NW + w);
+      const int i = r0 + lr - B.q16;  // row within V_q
+      if (i >= 0 && r0 + lr < r) {
+        const float* src = B.V + (int64_t)i * ldh + lc;
+        if (vec4 && lc + 4 <= B.kv) {
+          val = *reinterpret_cast<const f32x4*>(src);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) val[e] = (lc + e < kv) ? src[e] : 0.0f;
-      }
-      if (i < 16) {  // diagonal tile: unit lower-triangular mask
+          for (int e = 0; e < 4; ++e) val[e] = (lc + e < B.kv) ? src[e] : 0.0f;
+        }
+        if (i < 16) {  // diagonal tile: unit lower-triangular mask
 #pragma unroll
-        for (int e = 0; e < 4; ++e) val[e] = (lc + e > i) ? 0.0f : ((lc + e == i) ? 1.0f : val[e]);
+          for (int e = 0; e < 4; ++e)
+            val[e] = (lc + e > i) ? 0.0f : ((lc + e == i) ? 1.0f : val[e]);
+        }
       }
     }
-    *reinterpret_cast<f32x4*>(&vb[(tt * 16 + lr) * kVStride + lc]) = val;
+    ck.t[tt] = val;
   }
 }
 
-// c (a 16-column strip of r rows, strip layout) := (I - V T V^T)^T c for the
-// 16-wide reflector block V stored at Vq (its row 0 is strip row q16), T = Tq;
-// with kTransT = false, c := (I - V T V^T) c instead.
-// Three workgroup barriers; every thread of the workgroup must call it.
+template <int NW, int RL>
+__device__ __forceinline__ void put_v_chunk(float* __restrict__ vb, const VChunk<NW, RL>& ck,
+                                            int lane) {
+  constexpr int kStageTiles = StageTiles<NW, RL>::value;
+  const int lr = lane >> 2, lc = 4 * (lane & 3);
+#pragma unroll
+  for (int tt = 0; tt < kStageTiles; ++tt)
+    *reinterpret_cast<f32x4*>(&vb[(tt * 16 + lr) * kVStride + lc]) = ck.t[tt];
+}
+
+// c := (I - V T V^T)^T c (kTransT) or (I - V T V^T) c for block B with factor
+// Tq. On entry ck holds B's first chunk (from load_v_chunk); on return it holds
+// the first chunk of Bn if has_next.
+// Two workgroup barriers; every thread of the workgroup must call it.
 template <int NW, int RL, bool kTransT = true>
-__device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restrict__ Vq,
-                                           int64_t ldh, int q16, int r,
-                                           const float* __restrict__ Tq, WyShared<NW, RL>& sh,
-                                           int w, int lane, int kv = 16) {
+__device__ __forceinline__ void apply_wy16p(float (&c)[RL], VChunk<NW, RL>& ck, const VBlock& B,
+                                            const float* __restrict__ Tq, const VBlock& Bn,
+                                            bool has_next, int64_t ldh, int r,
+                                            WyPipeShared<NW, RL>& sh, int w, int lane) {
   using S = Strip<NW, RL>;
   constexpr int kStageTiles = StageTiles<NW, RL>::value;
   constexpr int kChunks = (S::kTiles + kStageTiles - 1) / kStageTiles;
   const int ii = lane & 15, kk = lane >> 4;
-  const bool vec4 = ((ldh & 3) == 0) && ((reinterpret_cast<uintptr_t>(Vq) & 15) == 0);
   float* vb = sh.vbuf[w];
-  if (threadIdx.x < 256) sh.ts[threadIdx.x >> 4][threadIdx.x & 15] = Tq[threadIdx.x];
+
+  // T in the A-operand layout of the W2 product: lane (ii, kk), K step v holds
+  // T[4 kk + v][ii] (W2 = T^T W) or T[ii][4 kk + v] (W2 = T W).
+  float ta[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int q = 4 * kk + v;  // only the upper triangle of T is read
+    ta[v] = kTransT ? ((q <= ii) ? Tq[q * 16 + ii] : 0.0f) : ((ii <= q) ? Tq[ii * 16 + q] : 0.0f);
+  }
 
   // W (16 x 16) = V^T c, partial over this wave's rows.
   f32x4 accw = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
-    stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4, kv);
+    if (ch > 0) wave_sync();  // the previous chunk's LDS reads are done
+    put_v_chunk<NW, RL>(vb, ck, lane);
     wave_sync();
+    // Next chunk to stage: the W phase runs chunks 0..kChunks-1, the update
+    // phase kChunks-1 (still in LDS) down to 0, then the next block's chunk 0.
+    if (ch + 1 < kChunks)
+      load_v_chunk<NW, RL>(ck, B, ldh, r, (ch + 1) * kStageTiles, w, lane);
+    else if (kChunks >= 2)
+      load_v_chunk<NW, RL>(ck, B, ldh, r, (kChunks - 2) * kStageTiles, w, lane);
+    else if (has_next)
+      load_v_chunk<NW, RL>(ck, Bn, ldh, r, 0, w, lane);
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
       const int t = ch * kStageTiles + tt;
       if (t >= S::kTiles) break;  // compile-time
-      // Tiles outside V_q or below the strip were staged as zeros: no branch
-      // here, so the compiler can batch the LDS reads.
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float av = vb[(tt * 16 + 4 * kk + v) * kVStride + ii];
         accw = __builtin_amdgcn_mfma_f32_16x16x4f32(av, c[4 * t + v], accw, 0, 0, 0);
       }
     }
-    if (kChunks > 1) wave_sync();
   }
-#pragma unroll
-  for (int v = 0; v < 4; ++v) sh.red[w][4 * kk + v][ii] = accw[v];
+  *reinterpret_cast<f32x4*>(&sh.red[w][4 * lane]) = accw;
   __syncthreads();
+  // The first 256 threads sum the NW partials of one element each (consecutive
+  // addresses: no bank conflicts), then every wave reads W back in the
+  // B-operand layout (lane (j, g), K step v: W[4 g + v][j]).
   if (threadIdx.x < 256) {
-    const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
-    float s = 0.0f;
+    float sum = sh.red[0][threadIdx.x];
 #pragma unroll
-    for (int u = 0; u < NW; ++u) s += sh.red[u][i][j];
-    sh.wsum[i][j] = s;
+    for (int u = 1; u < NW; ++u) sum += sh.red[u][threadIdx.x];
+    sh.wsum[threadIdx.x] = sum;
   }
   __syncthreads();
-  if (threadIdx.x < 256) {
-    // W2 = T^T W, or T W (T upper triangular)
-    const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
-    float s = 0.0f;
+  const f32x4 ws = *reinterpret_cast<const f32x4*>(&sh.wsum[4 * lane]);
+  // W2 in the accumulator layout: lane (ii, kk) holds W2[4 kk + s][ii] in w2[s].
+  f32x4 w2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      if constexpr (kTransT) {
-        if (q <= i) s = fmaf(sh.ts[q][i], sh.wsum[q][j], s);
-      } else {
-        if (q >= i) s = fmaf(sh.ts[i][q], sh.wsum[q][j], s);
-      }
-    }
-    sh.w2[i][j] = s;
-  }
-  __syncthreads();
+  for (int v = 0; v < 4; ++v) w2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[v], ws[v], w2, 0, 0, 0);
 
-  // c -= V W2, with the K (reflector) order permuted so that lane (ii, kk)
-  // reads V[row ii][4kk .. 4kk+3] as one b128 and W2[4kk + s][ii].
-  float bw[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) bw[s] = sh.w2[4 * kk + s][ii];
+  // c -= V W2, K order permuted so that lane (ii, kk) reads V[row ii][4kk..4kk+3]
+  // as one b128 and uses W2[4kk + s][ii] = w2[s].
 #pragma unroll
   for (int ch = kChunks - 1; ch >= 0; --ch) {
     if (ch != kChunks - 1) {
       wave_sync();
-      stage_v<NW, RL>(vb, Vq, ldh, q16, r, ch * kStageTiles, w, lane, vec4, kv);
+      put_v_chunk<NW, RL>(vb, ck, lane);
       wave_sync();
+      if (ch >= 1)
+        load_v_chunk<NW, RL>(ck, B, ldh, r, (ch - 1) * kStageTiles, w, lane);
+      else if (has_next)
+        load_v_chunk<NW, RL>(ck, Bn, ldh, r, 0, w, lane);
     }
 #pragma unroll
     for (int tt = 0; tt < kStageTiles; ++tt) {
@@ -193,12 +240,12 @@ __device__ __forceinline__ void apply_wy16(float (&c)[RL], const float* __restri
       f32x4 acc = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-a4[s], bw[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-a4[s], w2[s], acc, 0, 0, 0);
 #pragma unroll
       for (int v = 0; v < 4; ++v) c[4 * t + v] = acc[v];
     }
   }
-  __syncthreads();  // sh is reused by the next call
+  wave_sync();  // this wave's LDS chunk is rewritten by the next call
 }
 
 template <int NW, int RL>
@@ -272,7 +319,7 @@ __device__ __forceinline__ void publish_x(float* __restrict__ xw, const float (&
 // Shared memory of k_panel.
 template <int NW, int RL>
 struct PanelShared {
-  WyShared<NW, RL> wy;
+  WyPipeShared<NW, RL> wy;
   alignas(16) float xs[NW][4 * RL];  // per-wave x slab of the general pass
   // Row stride 4 NW + 4: the b128 reads of 16 columns land on distinct banks.
   alignas(16) float red[2][16][4 * NW + 4];
@@ -496,11 +543,14 @@ template <int NW, int RL>
 __device__ __forceinline__ void panel_load_apply(float (&c)[RL], const float* __restrict__ Blk,
                                                  int64_t ldh, int p, int r, int kw,
                                                  const float* __restrict__ Tb,
-                                                 WyShared<NW, RL>& wy, int w, int lane) {
+                                                 WyPipeShared<NW, RL>& wy, int w, int lane) {
+  auto block = [&](int q) { return VBlock{Blk + (int64_t)(16 * q) * ldh + 16 * q, 16 * q, 16}; };
+  VChunk<NW, RL> ck;
+  if (p > 0) load_v_chunk<NW, RL>(ck, block(0), ldh, r, 0, w, lane);
   load_strip<NW, RL>(c, Blk + 16 * p, ldh, r, kw, w, lane);
   for (int q = 0; q < p; ++q)
-    apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q,
-                       wy, w, lane);
+    apply_wy16p<NW, RL>(c, ck, block(q), Tb + 256 * q, block(q + 1 < p ? q + 1 : q), q + 1 < p, ldh,
+                        r, wy, w, lane);
 }
 
 // The fast pass can be switched off (every panel then takes the general pass).
@@ -616,7 +666,7 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
                                                    int64_t ldh, int J0, int nblk, int r, int c0,
                                                    int ncols, const float* __restrict__ Tws,
                                                    int64_t sTwb) {
-  __shared__ WyShared<NW, RL> wy;
+  __shared__ WyPipeShared<NW, RL> wy;
   const int nstrips = (ncols + 15) / 16;
   const int id = xcd_logical_id(blockIdx.x, gridDim.x);
   const int b = id / nstrips;
@@ -627,12 +677,15 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   float* P = Blk + c0 + s0;
   const float* Tb = Tws + (int64_t)b * sTwb;
   const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
+  auto block = [&](int q) { return VBlock{Blk + (int64_t)(16 * q) * ldh + 16 * q, 16 * q, 16}; };
 
   float c[RL];
+  VChunk<NW, RL> ck;
+  load_v_chunk<NW, RL>(ck, block(0), ldh, r, 0, w, lane);
   load_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
   for (int q = 0; q < nblk; ++q)
-    apply_wy16<NW, RL>(c, Blk + (int64_t)(16 * q) * ldh + 16 * q, ldh, 16 * q, r, Tb + 256 * q, wy,
-                       w, lane);
+    apply_wy16p<NW, RL>(c, ck, block(q), Tb + 256 * q, block(q + 1 < nblk ? q + 1 : q),
+                        q + 1 < nblk, ldh, r, wy, w, lane);
   store_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
 }
 
@@ -647,7 +700,7 @@ __global__ __launch_bounds__(64 * NW) void k_apply(const float* __restrict__ V, 
                                                    int64_t sCb, int64_t ldc, int nblk, int r,
                                                    int ncols, const float* __restrict__ Tws,
                                                    int64_t sTwb, int kv_last) {
-  __shared__ WyShared<NW, RL> wy;
+  __shared__ WyPipeShared<NW, RL> wy;
   const int nstrips = (ncols + 15) / 16;
   const int id = xcd_logical_id(blockIdx.x, gridDim.x);
   const int b = id / nstrips;
@@ -658,13 +711,20 @@ __global__ __launch_bounds__(64 * NW) void k_apply(const float* __restrict__ V, 
   float* P = C + (int64_t)b * sCb + s0;
   const float* Tb = Tws + (int64_t)b * sTwb;
   const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
+  // i-th block applied: q = i (Q^T C) or nblk - 1 - i (Q C).
+  auto block = [&](int i) {
+    const int q = kTrans ? i : nblk - 1 - i;
+    return VBlock{Vb + (int64_t)(16 * q) * ldv + 16 * q, 16 * q, q == nblk - 1 ? kv_last : 16};
+  };
 
   float c[RL];
+  VChunk<NW, RL> ck;
+  load_v_chunk<NW, RL>(ck, block(0), ldv, r, 0, w, lane);
   load_strip<NW, RL>(c, P, ldc, r, ncol, w, lane);
   for (int i = 0; i < nblk; ++i) {
     const int q = kTrans ? i : nblk - 1 - i;
-    apply_wy16<NW, RL, kTrans>(c, Vb + (int64_t)(16 * q) * ldv + 16 * q, ldv, 16 * q, r,
-                               Tb + 256 * q, wy, w, lane, q == nblk - 1 ? kv_last : 16);
+    apply_wy16p<NW, RL, kTrans>(c, ck, block(i), Tb + 256 * q, block(i + 1 < nblk ? i + 1 : i),
+                                i + 1 < nblk, ldv, r, wy, w, lane);
   }
   store_strip<NW, RL>(c, P, ldc, r, ncol, w, lane);
 }

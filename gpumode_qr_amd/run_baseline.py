@@ -10,18 +10,32 @@ codes follow :66-252):
 
 Exit codes: 0 all gates pass, 1 no torch / no GPU, 2 a gate failed.
 ``--configs`` selects the five headline configs instead of the official shapes.
+
+The record keeps the reference's schema (dbwrite.py:61-93): each
+``benchmark_results`` entry holds exactly ``shape``, ``name``, ``correctness`` and
+``timing``. The fields the reference does not have go under ``extra``:
+``per_shape`` (GFLOP/s, % of the MI355X FP32 matrix peak, the CPU ``torch.geqrf``
+time with ``--cpu-baseline``, and this library's per-kernel launch counters),
+``cpu_cores`` and ``fp32_peak_gflops``.
 """
 
 from __future__ import annotations
 
 import argparse
+import os
+import statistics
 import sys
+import time
 from pathlib import Path
 
 from .variants import CHAMPION, VARIANTS as _VARIANTS, format_variant_list
 
 REPO_ROOT = Path(__file__).resolve().parents[1]
 BASELINE = "torch_geqrf"
+# MI355X dense FP32 matrix (MFMA) peak, GFLOP/s.
+FP32_PEAK_GFLOPS = 157_300.0
+# Calls traced per shape for the per-kernel counters.
+COUNTER_CALLS = 3
 ALL_IMPLS = sorted(set(_VARIANTS) | {BASELINE})
 
 try:  # torch is needed only for the benchmarking paths, not for --list
@@ -75,9 +89,58 @@ def run_correctness_stress(fn, device: str) -> list[dict]:
     return results
 
 
+def cpu_cores() -> int:
+    """Cores torch's CPU geqrf may use: all the cores this process may run on."""
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_geqrf_ms(A: torch.Tensor, reps: int = 3) -> float:
+    """Median wall time of torch.geqrf (MKL) on a CPU copy of A, all cores."""
+    torch.set_num_threads(cpu_cores())
+    Ac = A.detach().to("cpu")
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        torch.geqrf(Ac)
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+def kernel_counters(fn, A: torch.Tensor, calls: int = COUNTER_CALLS) -> dict:
+    """Per-kernel launches, time and algorithmic rates per call of fn(A), from the
+    library's launch tracer (HIP events around each launch of its kernels)."""
+    from . import _lib
+
+    names = list(_lib.KERNELS)
+    _lib.trace_reset()
+    _lib.trace_enable(names)
+    try:
+        for _ in range(calls):
+            fn(A)
+        torch.cuda.synchronize()
+    finally:
+        _lib.trace_enable(None)
+    out = {}
+    for nm in names:
+        d = _lib.trace_read(nm)
+        if not d["launches"]:
+            continue
+        sec = d["ms"] * 1e-3
+        out[nm] = {
+            "launches_per_call": d["launches"] / calls,
+            "ms_per_call": d["ms"] / calls,
+            "tflops": d["flops"] / sec / 1e12 if sec > 0 else 0.0,
+            "gbs": d["bytes"] / sec / 1e9 if sec > 0 else 0.0,
+        }
+    _lib.trace_reset()
+    return out
+
+
 def run_benchmarks(fn, device: str, warmup: int, iters: int, shapes: list[dict] | None = None,
-                   configs: list[int] | None = None) -> list[dict]:
-    results = []
+                   configs: list[int] | None = None, cpu_baseline: bool = False,
+                   counters: bool = False) -> tuple[list[dict], list[dict]]:
+    """Returns (benchmark_results in the reference's schema, per-shape extras)."""
+    results, extras = [], []
     for prob in _problems(shapes, configs, device):
         H, tau = fn(prob.tensor)
         torch.cuda.synchronize()
@@ -91,15 +154,21 @@ def run_benchmarks(fn, device: str, warmup: int, iters: int, shapes: list[dict] 
             "name": prob.name,
             "correctness": chk.as_dict(),
             "timing": timing.as_dict(),
-            "gflops": gflops,
         })
+        ext = {"name": prob.name, "gflops": gflops, "pct_peak": 100.0 * gflops / FP32_PEAK_GFLOPS}
+        if cpu_baseline:
+            ext["cpu_geqrf_ms"] = cpu_geqrf_ms(prob.tensor)
+        if counters:
+            ext["counters"] = kernel_counters(fn, prob.tensor)
+        extras.append(ext)
         status = "PASS" if chk.passed else "FAIL"
+        cpu = f" cpu={ext['cpu_geqrf_ms']:.1f}ms" if cpu_baseline else ""
         print(f"[bench] {prob.name:>28} {status} median={timing.median:.3f}ms "
-              f"min={timing.min:.3f}ms {gflops:.0f} GFLOP/s "
-              f"factor={chk.factor_residual:.2e} orth={chk.orth_residual:.2e}")
+              f"min={timing.min:.3f}ms {gflops:.0f} GFLOP/s ({ext['pct_peak']:.1f}% peak)"
+              f"{cpu} factor={chk.factor_residual:.2e} orth={chk.orth_residual:.2e}")
     gm = bench.geomean([r["timing"]["median_ms"] for r in results])
     print(f"[bench] geomean(median) across {len(results)} problems = {gm:.4f} ms")
-    return results
+    return results, extras
 
 
 def run_compare(impls: list[str], device: str, warmup: int, iters: int, shapes, configs) -> int:
@@ -107,7 +176,7 @@ def run_compare(impls: list[str], device: str, warmup: int, iters: int, shapes, 
     summary = []
     for impl in impls:
         print(f"=== {impl}{'  (champion)' if impl == CHAMPION else ''} ===")
-        res = run_benchmarks(REGISTRY[impl], device, warmup, iters, shapes, configs)
+        res, _ = run_benchmarks(REGISTRY[impl], device, warmup, iters, shapes, configs)
         gm = bench.geomean([r["timing"]["median_ms"] for r in res])
         summary.append((impl, gm, all(r["correctness"]["passed"] for r in res)))
         print()
@@ -136,6 +205,8 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--impls", default=None, help="comma-separated impls for --compare")
     ap.add_argument("--shapes", default=None, help="official shapes by name or n (default: all 7)")
     ap.add_argument("--configs", default=None, help="headline configs, e.g. 2,3,4,5")
+    ap.add_argument("--cpu-baseline", action="store_true",
+                    help="also time torch.geqrf on CPU copies of each input (extra.per_shape)")
     args = ap.parse_args(argv)
 
     if args.list:
@@ -162,7 +233,9 @@ def main(argv: list[str] | None = None) -> int:
     print(f"impl={args.impl} device={torch.cuda.get_device_name(0)} "
           f"torch={torch.__version__} hip={torch.version.hip}")
     stress = run_correctness_stress(fn, args.device) if args.stress else []
-    results = run_benchmarks(fn, args.device, args.warmup, args.iters, shapes, configs)
+    results, per_shape = run_benchmarks(fn, args.device, args.warmup, args.iters, shapes,
+                                        configs, cpu_baseline=args.cpu_baseline,
+                                        counters=args.impl in _VARIANTS)
     all_pass = all(r["correctness"]["passed"] for r in results)
     stress_pass = all(r["passed"] for r in stress) if stress else None
     gm_med = bench.geomean([r["timing"]["median_ms"] for r in results])
@@ -177,6 +250,9 @@ def main(argv: list[str] | None = None) -> int:
             "stress_results": stress,
             "geomean_median_ms": gm_med,
             "geomean_min_ms": gm_min,
+            "per_shape": per_shape,
+            "cpu_cores": cpu_cores() if args.cpu_baseline else None,
+            "fp32_peak_gflops": FP32_PEAK_GFLOPS,
         })
         print(f"wrote {path}")
     return 0 if all_pass and (stress_pass is not False) else 2

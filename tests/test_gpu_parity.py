@@ -403,3 +403,36 @@ def test_variant_registry_runs_hip_path():
     H, tau = VARIANTS[CHAMPION](A)
     torch.cuda.synchronize()
     assert checker.check(A, H, tau).passed
+
+
+def test_run_baseline_db_record_schema(tmp_path):
+    """The DB record keeps the reference's keys (dbwrite.py:61-93; each
+    benchmark_results entry: shape, name, correctness, timing) and carries the new
+    per-shape fields under extra."""
+    import json
+
+    from gpumode_qr_amd import run_baseline
+
+    _say("run_baseline --configs 1 --cpu-baseline (DB record)")
+    rc = run_baseline.main(["--configs", "1", "--warmup", "1", "--iters", "3", "--cpu-baseline",
+                            "--db-dir", str(tmp_path)])
+    assert rc == 0
+    (path,) = list(tmp_path.glob("*_hh_mi355x.json"))
+    rec = json.loads(path.read_text())
+    assert list(rec) == ["impl", "git_commit", "date", "rocm_version", "docker_image",
+                         "torch_version", "gpu_name", "hip_visible_devices",
+                         "benchmark_results", "extra"]
+    (res,) = rec["benchmark_results"]
+    assert list(res) == ["shape", "name", "correctness", "timing"]
+    assert res["correctness"]["passed"]
+    extra = rec["extra"]
+    for key in ("warmup", "iters", "all_benchmarks_pass", "stress_pass", "stress_results"):
+        assert key in extra  # the reference's own extra keys
+    (ps,) = extra["per_shape"]
+    assert ps["name"] == res["name"]
+    gflops = 4.0 / 3.0 * 32**3 * 64 / (res["timing"]["median_ms"] * 1e-3) / 1e9
+    assert ps["gflops"] == pytest.approx(gflops, rel=1e-9)
+    assert ps["pct_peak"] == pytest.approx(100.0 * gflops / 157_300.0, rel=1e-9)
+    assert ps["cpu_geqrf_ms"] > 0 and extra["cpu_cores"] >= 1
+    assert ps["counters"]["smalln"]["launches_per_call"] == 1.0
+    assert set(ps["counters"]) == {"smalln"}  # n = 32 runs the one fused launch
