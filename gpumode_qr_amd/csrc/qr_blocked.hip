@@ -386,7 +386,7 @@ __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, 
     const float alpha = readlane_f(e, J);
     const bool ident = dj >= r - 1;  // no rows below the diagonal
     ok = ok && (ident || reflector_fast_ok(alpha, sigma));
-    Reflector R = reflector_fast(alpha, sigma);
+    Reflector R = reflector_fast_rcp(alpha, sigma);
     if (ident) R = reflector_identity(alpha);
     const float wk = fmaf(R.gamma, ds, e);  // v_J^T c_k
     const float cc = R.tau * wk;
@@ -595,12 +595,27 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
     panel_general_pass<NW, RL>(c, sh, p, r, kw, w, lane, st);
   }
   const int d0 = 16 * p;
-  if (w == 0 && g == 0) sh.taus[k] = (k < kw) ? st.tau : 0.0f;
-  __syncthreads();
+
+  // Write back first: R above the diagonal, beta on it, v = (x pre) gamma
+  // below. The stores drain while wave 0 forms T.
+  const int kd = d0 + k;
+#pragma unroll
+  for (int t = 0; t < S::kTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = S::row(t, v, w, g);
+      c[4 * t + v] =
+          (row < kd) ? c[4 * t + v] : ((row == kd) ? st.beta : (c[4 * t + v] * st.pre) * st.gamma);
+    }
+  store_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
 
   // T_p (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
   // Lane k of wave 0 holds row k of T in registers; z_j rows are b128 reads.
-  if (w == 0 && g == 0) {
+  // Only wave 0 wrote zbuf and writes taus, so a wave-level sync suffices.
+  if (w != 0) return;
+  if (g == 0) sh.taus[k] = (k < kw) ? st.tau : 0.0f;
+  wave_sync();
+  if (g == 0) {
     float trow[16];
     const float tk = sh.taus[k];
 #pragma unroll
@@ -629,18 +644,6 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
     for (int q = 0; q < 16; ++q) Tp[k * 16 + q] = trow[q];
     if (k < kw) tau[(int64_t)b * sTaub + J0 + d0 + k] = st.tau;
   }
-
-  // Write back: R above the diagonal, beta on it, v = (x pre) gamma below.
-  const int kd = d0 + k;
-#pragma unroll
-  for (int t = 0; t < S::kTiles; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = S::row(t, v, w, g);
-      c[4 * t + v] =
-          (row < kd) ? c[4 * t + v] : ((row == kd) ? st.beta : (c[4 * t + v] * st.pre) * st.gamma);
-    }
-  store_strip<NW, RL>(c, P, ldh, r, kw, w, lane);
 }
 
 // The dispatcher hands workgroup i to XCD i mod kXcds, and each XCD has its
