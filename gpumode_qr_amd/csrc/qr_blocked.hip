@@ -98,12 +98,13 @@ struct VBlock {
   int kv;
 };
 
-// LDS of apply_wy16p: per-wave V chunks, the NW partial W's and their sum.
-template <int NW, int RL>
+// LDS of apply_wy16p for KS strips: per-wave V chunks, the NW partial W's of
+// each strip and their sums.
+template <int NW, int RL, int KS = 1>
 struct WyPipeShared {
   float vbuf[NW][StageTiles<NW, RL>::value * 16 * kVStride];
-  alignas(16) float red[NW][64 * 4];
-  alignas(16) float wsum[64 * 4];
+  alignas(16) float red[KS][NW][64 * 4];
+  alignas(16) float wsum[KS][64 * 4];
 };
 
 // Global loads of this wave's tiles [t0, t0 + kStageTiles) of block B: rows
@@ -151,15 +152,16 @@ __device__ __forceinline__ void put_v_chunk(float* __restrict__ vb, const VChunk
     *reinterpret_cast<f32x4*>(&vb[(tt * 16 + lr) * kVStride + lc]) = ck.t[tt];
 }
 
-// c := (I - V T V^T)^T c (kTransT) or (I - V T V^T) c for block B with factor
-// Tq. On entry ck holds B's first chunk (from load_v_chunk); on return it holds
-// the first chunk of Bn if has_next.
+// c[s] := (I - V T V^T)^T c[s] (kTransT) or (I - V T V^T) c[s], s < KS, for
+// block B with factor Tq: KS 16-column strips share every V read and every
+// barrier. On entry ck holds B's first chunk (from load_v_chunk); on return it
+// holds the first chunk of Bn if has_next.
 // Two workgroup barriers; every thread of the workgroup must call it.
-template <int NW, int RL, bool kTransT = true>
-__device__ __forceinline__ void apply_wy16p(float (&c)[RL], VChunk<NW, RL>& ck, const VBlock& B,
-                                            const float* __restrict__ Tq, const VBlock& Bn,
-                                            bool has_next, int64_t ldh, int r,
-                                            WyPipeShared<NW, RL>& sh, int w, int lane) {
+template <int NW, int RL, int KS, bool kTransT = true>
+__device__ __forceinline__ void apply_wy16p(float (&c)[KS][RL], VChunk<NW, RL>& ck,
+                                            const VBlock& B, const float* __restrict__ Tq,
+                                            const VBlock& Bn, bool has_next, int64_t ldh, int r,
+                                            WyPipeShared<NW, RL, KS>& sh, int w, int lane) {
   using S = Strip<NW, RL>;
   constexpr int kStageTiles = StageTiles<NW, RL>::value;
   constexpr int kChunks = (S::kTiles + kStageTiles - 1) / kStageTiles;
@@ -175,8 +177,10 @@ __device__ __forceinline__ void apply_wy16p(float (&c)[RL], VChunk<NW, RL>& ck, 
     ta[v] = kTransT ? ((q <= ii) ? Tq[q * 16 + ii] : 0.0f) : ((ii <= q) ? Tq[ii * 16 + q] : 0.0f);
   }
 
-  // W (16 x 16) = V^T c, partial over this wave's rows.
-  f32x4 accw = {0.0f, 0.0f, 0.0f, 0.0f};
+  // W (16 x 16 per strip) = V^T c, partial over this wave's rows.
+  f32x4 accw[KS];
+#pragma unroll
+  for (int st = 0; st < KS; ++st) accw[st] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
     if (ch > 0) wave_sync();  // the previous chunk's LDS reads are done
@@ -197,30 +201,40 @@ __device__ __forceinline__ void apply_wy16p(float (&c)[RL], VChunk<NW, RL>& ck, 
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float av = vb[(tt * 16 + 4 * kk + v) * kVStride + ii];
-        accw = __builtin_amdgcn_mfma_f32_16x16x4f32(av, c[4 * t + v], accw, 0, 0, 0);
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+          accw[st] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, c[st][4 * t + v], accw[st], 0, 0, 0);
       }
     }
   }
-  *reinterpret_cast<f32x4*>(&sh.red[w][4 * lane]) = accw;
-  __syncthreads();
-  // The first 256 threads sum the NW partials of one element each (consecutive
-  // addresses: no bank conflicts), then every wave reads W back in the
-  // B-operand layout (lane (j, g), K step v: W[4 g + v][j]).
-  if (threadIdx.x < 256) {
-    float sum = sh.red[0][threadIdx.x];
 #pragma unroll
-    for (int u = 1; u < NW; ++u) sum += sh.red[u][threadIdx.x];
-    sh.wsum[threadIdx.x] = sum;
+  for (int st = 0; st < KS; ++st) *reinterpret_cast<f32x4*>(&sh.red[st][w][4 * lane]) = accw[st];
+  __syncthreads();
+  // Each of the first 256 KS threads sums the NW partials of one element
+  // (consecutive addresses: no bank conflicts); then every wave reads W back in
+  // the B-operand layout (lane (j, g), K step v: W[4 g + v][j]).
+  static_assert(KS * 256 <= 64 * NW, "one summing thread per element of W");
+  if (threadIdx.x < KS * 256) {
+    const int st = KS == 1 ? 0 : threadIdx.x >> 8, el = threadIdx.x & 255;
+    float sum = sh.red[st][0][el];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) sum += sh.red[st][u][el];
+    sh.wsum[st][el] = sum;
   }
   __syncthreads();
-  const f32x4 ws = *reinterpret_cast<const f32x4*>(&sh.wsum[4 * lane]);
-  // W2 in the accumulator layout: lane (ii, kk) holds W2[4 kk + s][ii] in w2[s].
-  f32x4 w2 = {0.0f, 0.0f, 0.0f, 0.0f};
+  // W2 in the accumulator layout: lane (ii, kk) holds W2[4 kk + s][ii] in w2[.][s].
+  f32x4 w2[KS];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) w2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[v], ws[v], w2, 0, 0, 0);
+  for (int st = 0; st < KS; ++st) {
+    const f32x4 ws = *reinterpret_cast<const f32x4*>(&sh.wsum[st][4 * lane]);
+    w2[st] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      w2[st] = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[v], ws[v], w2[st], 0, 0, 0);
+  }
 
   // c -= V W2, K order permuted so that lane (ii, kk) reads V[row ii][4kk..4kk+3]
-  // as one b128 and uses W2[4kk + s][ii] = w2[s].
+  // as one b128 and uses W2[4kk + s][ii] = w2[.][s].
 #pragma unroll
   for (int ch = kChunks - 1; ch >= 0; --ch) {
     if (ch != kChunks - 1) {
@@ -237,12 +251,15 @@ __device__ __forceinline__ void apply_wy16p(float (&c)[RL], VChunk<NW, RL>& ck, 
       const int t = ch * kStageTiles + tt;
       if (t >= S::kTiles) break;  // compile-time
       const f32x4 a4 = *reinterpret_cast<const f32x4*>(&vb[(tt * 16 + ii) * kVStride + 4 * kk]);
-      f32x4 acc = {c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-a4[s], w2[s], acc, 0, 0, 0);
+      for (int st = 0; st < KS; ++st) {
+        f32x4 acc = {c[st][4 * t], c[st][4 * t + 1], c[st][4 * t + 2], c[st][4 * t + 3]};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) c[4 * t + v] = acc[v];
+        for (int q = 0; q < 4; ++q)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(-a4[q], w2[st][q], acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) c[st][4 * t + v] = acc[v];
+      }
     }
   }
   wave_sync();  // this wave's LDS chunk is rewritten by the next call
@@ -540,17 +557,17 @@ __device__ __forceinline__ void panel_general_pass(float (&c)[RL], PanelShared<N
 // c := panel p (kw columns at Blk + 16 p, r rows, strip layout) after the
 // left-looking update with panels 0..p-1 of the outer block at Blk.
 template <int NW, int RL>
-__device__ __forceinline__ void panel_load_apply(float (&c)[RL], const float* __restrict__ Blk,
+__device__ __forceinline__ void panel_load_apply(float (&c)[1][RL], const float* __restrict__ Blk,
                                                  int64_t ldh, int p, int r, int kw,
                                                  const float* __restrict__ Tb,
                                                  WyPipeShared<NW, RL>& wy, int w, int lane) {
   auto block = [&](int q) { return VBlock{Blk + (int64_t)(16 * q) * ldh + 16 * q, 16 * q, 16}; };
   VChunk<NW, RL> ck;
   if (p > 0) load_v_chunk<NW, RL>(ck, block(0), ldh, r, 0, w, lane);
-  load_strip<NW, RL>(c, Blk + 16 * p, ldh, r, kw, w, lane);
+  load_strip<NW, RL>(c[0], Blk + 16 * p, ldh, r, kw, w, lane);
   for (int q = 0; q < p; ++q)
-    apply_wy16p<NW, RL>(c, ck, block(q), Tb + 256 * q, block(q + 1 < p ? q + 1 : q), q + 1 < p, ldh,
-                        r, wy, w, lane);
+    apply_wy16p<NW, RL, 1>(c, ck, block(q), Tb + 256 * q, block(q + 1 < p ? q + 1 : q), q + 1 < p,
+                           ldh, r, wy, w, lane);
 }
 
 // The fast pass can be switched off (every panel then takes the general pass).
@@ -580,8 +597,9 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
 
   // The panel after the left-looking update with panels 0..p-1; the panel in
   // HBM is not written before the end, so the general pass can start over.
-  float c[RL];
-  panel_load_apply<NW, RL>(c, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
+  float cs[1][RL];
+  float (&c)[RL] = cs[0];
+  panel_load_apply<NW, RL>(cs, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
 
   PanelCol st;
   bool ok = false;
@@ -589,7 +607,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   if (!ok) [[unlikely]] {
     if constexpr (kPanelFastPass) {
       __syncthreads();  // every wave is past its last read of erow / red
-      panel_load_apply<NW, RL>(c, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
+      panel_load_apply<NW, RL>(cs, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
       st = PanelCol{};
     }
     panel_general_pass<NW, RL>(c, sh, p, r, kw, w, lane, st);
@@ -661,35 +679,46 @@ __device__ __forceinline__ int xcd_logical_id(int id, int total) {
 
 // Columns c0.. c0+ncols-1 (relative to the outer block at J0, r rows) :=
 // Q^T C with the nblk 16-wide reflector blocks of the outer block, applied
-// in order 0..nblk-1. 1-D grid of nstrips * batch workgroups, nstrips =
-// ceil(ncols / 16); one strip per workgroup, strip-major within a matrix
-// after the XCD renumbering.
-template <int NW, int RL>
+// in order 0..nblk-1. Each workgroup updates KS adjacent 16-column strips;
+// 1-D grid of ngroups * batch workgroups, ngroups = ceil(ncols / (16 KS)),
+// group-major within a matrix after the XCD renumbering.
+template <int NW, int RL, int KS>
 __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_t sHb,
                                                    int64_t ldh, int J0, int nblk, int r, int c0,
                                                    int ncols, const float* __restrict__ Tws,
                                                    int64_t sTwb) {
-  __shared__ WyPipeShared<NW, RL> wy;
-  const int nstrips = (ncols + 15) / 16;
+  __shared__ WyPipeShared<NW, RL, KS> wy;
+  const int ngroups = (ncols + 16 * KS - 1) / (16 * KS);
   const int id = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int b = id / nstrips;
+  const int b = id / ngroups;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
-  const int s0 = 16 * (id - b * nstrips);
+  const int s0 = 16 * KS * (id - b * ngroups);
   float* P = Blk + c0 + s0;
   const float* Tb = Tws + (int64_t)b * sTwb;
-  const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
   auto block = [&](int q) { return VBlock{Blk + (int64_t)(16 * q) * ldh + 16 * q, 16 * q, 16}; };
+  // Columns of strip st inside the matrix (<= 0: strip past the last column).
+  auto ncol = [&](int st) {
+    const int left = ncols - s0 - 16 * st;
+    return left < 16 ? left : 16;
+  };
 
-  float c[RL];
+  float c[KS][RL];
   VChunk<NW, RL> ck;
+#pragma unroll
+  for (int st = 0; st < KS; ++st) load_strip<NW, RL>(c[st], P + 16 * st, ldh, r, ncol(st), w, lane);
+  // The strip's loads are issued (and their 64-bit addresses dead) before the
+  // first V chunk's: the compiler would otherwise keep every address live at
+  // once and spill.
+  asm volatile("" ::: "memory");
   load_v_chunk<NW, RL>(ck, block(0), ldh, r, 0, w, lane);
-  load_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
   for (int q = 0; q < nblk; ++q)
-    apply_wy16p<NW, RL>(c, ck, block(q), Tb + 256 * q, block(q + 1 < nblk ? q + 1 : q),
-                        q + 1 < nblk, ldh, r, wy, w, lane);
-  store_strip<NW, RL>(c, P, ldh, r, ncol, w, lane);
+    apply_wy16p<NW, RL, KS>(c, ck, block(q), Tb + 256 * q, block(q + 1 < nblk ? q + 1 : q),
+                            q + 1 < nblk, ldh, r, wy, w, lane);
+#pragma unroll
+  for (int st = 0; st < KS; ++st)
+    store_strip<NW, RL>(c[st], P + 16 * st, ldh, r, ncol(st), w, lane);
 }
 
 // Apply nblk 16-wide reflector blocks (V_q at V + 16 q (ldv + 1) of each matrix,
@@ -697,40 +726,61 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
 // Q^T C with blocks in order 0..nblk-1 (kTrans), or C := Q C with blocks in order
 // nblk-1..0, Q = (I - V_0 T_0 V_0^T) ... (I - V_{nblk-1} T_{nblk-1} V^T). 1-D grid
 // of nstrips * batch workgroups, XCD-aware like k_trail.
-template <int NW, int RL, bool kTrans>
+template <int NW, int RL, int KS, bool kTrans>
 __global__ __launch_bounds__(64 * NW) void k_apply(const float* __restrict__ V, int64_t sVb,
                                                    int64_t ldv, float* __restrict__ C,
                                                    int64_t sCb, int64_t ldc, int nblk, int r,
                                                    int ncols, const float* __restrict__ Tws,
                                                    int64_t sTwb, int kv_last) {
-  __shared__ WyPipeShared<NW, RL> wy;
-  const int nstrips = (ncols + 15) / 16;
+  __shared__ WyPipeShared<NW, RL, KS> wy;
+  const int ngroups = (ncols + 16 * KS - 1) / (16 * KS);
   const int id = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int b = id / nstrips;
+  const int b = id / ngroups;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const float* Vb = V + (int64_t)b * sVb;
-  const int s0 = 16 * (id - b * nstrips);
+  const int s0 = 16 * KS * (id - b * ngroups);
   float* P = C + (int64_t)b * sCb + s0;
   const float* Tb = Tws + (int64_t)b * sTwb;
-  const int ncol = (ncols - s0) < 16 ? (ncols - s0) : 16;
+  auto ncol = [&](int st) {
+    const int left = ncols - s0 - 16 * st;
+    return left < 16 ? left : 16;
+  };
   // i-th block applied: q = i (Q^T C) or nblk - 1 - i (Q C).
   auto block = [&](int i) {
     const int q = kTrans ? i : nblk - 1 - i;
     return VBlock{Vb + (int64_t)(16 * q) * ldv + 16 * q, 16 * q, q == nblk - 1 ? kv_last : 16};
   };
 
-  float c[RL];
+  float c[KS][RL];
   VChunk<NW, RL> ck;
+#pragma unroll
+  for (int st = 0; st < KS; ++st) load_strip<NW, RL>(c[st], P + 16 * st, ldc, r, ncol(st), w, lane);
+  asm volatile("" ::: "memory");  // as in k_trail
   load_v_chunk<NW, RL>(ck, block(0), ldv, r, 0, w, lane);
-  load_strip<NW, RL>(c, P, ldc, r, ncol, w, lane);
   for (int i = 0; i < nblk; ++i) {
     const int q = kTrans ? i : nblk - 1 - i;
-    apply_wy16p<NW, RL, kTrans>(c, ck, block(i), Tb + 256 * q, block(i + 1 < nblk ? i + 1 : i),
-                                i + 1 < nblk, ldv, r, wy, w, lane);
+    apply_wy16p<NW, RL, KS, kTrans>(c, ck, block(i), Tb + 256 * q,
+                                    block(i + 1 < nblk ? i + 1 : i), i + 1 < nblk, ldv, r, wy, w,
+                                    lane);
   }
-  store_strip<NW, RL>(c, P, ldc, r, ncol, w, lane);
+#pragma unroll
+  for (int st = 0; st < KS; ++st)
+    store_strip<NW, RL>(c[st], P + 16 * st, ldc, r, ncol(st), w, lane);
 }
+
+// Strips per workgroup of the trailing update / Q application: two for the
+// 16-wave workgroups of up to 1024 rows (a wave's share of two strips fits
+// the 128-VGPR budget of 4 waves per SIMD), else one. Eight-wave workgroups
+// (r <= 512) keep one strip: there the lower register count buys a third
+// resident workgroup per CU, which measured faster.
+#ifndef QR_TRAIL_KS_MAX
+#define QR_TRAIL_KS_MAX 2
+#endif
+template <int NW, int RL>
+struct TrailKS {
+  static constexpr int value = (NW >= 16 && RL <= 16 && QR_TRAIL_KS_MAX >= 2) ? 2 : 1;
+};
 
 // (NW, RL) for r rows: 4 NW RL >= r and NW > p for every panel index used.
 #define QR_STRIP_DISPATCH(r, CASE)   \
@@ -777,12 +827,14 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
   if (ncols <= 0) return hipSuccess;
   if (nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || r < 16 * (nblk - 1) + 1)
     return hipErrorInvalidValue;
-  const int64_t wgs = (int64_t)((ncols + 15) / 16) * batch;
-  if (wgs > INT32_MAX) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)wgs);
-#define QR_TRAIL_CASE(NWV, RLV)                                                              \
-  hipLaunchKernelGGL((k_trail<NWV, RLV>), grid, dim3(64 * NWV), 0, stream, H, sHb, ldh, J0, \
-                     nblk, r, c0, ncols, Tws, sTwb)
+  if ((int64_t)((ncols + 15) / 16) * batch > INT32_MAX) return hipErrorInvalidValue;
+#define QR_TRAIL_CASE(NWV, RLV)                                                                 \
+  do {                                                                                          \
+    constexpr int KS = TrailKS<NWV, RLV>::value;                                                \
+    const dim3 grid((unsigned)((ncols + 16 * KS - 1) / (16 * KS) * (int64_t)batch));           \
+    hipLaunchKernelGGL((k_trail<NWV, RLV, KS>), grid, dim3(64 * NWV), 0, stream, H, sHb, ldh,  \
+                       J0, nblk, r, c0, ncols, Tws, sTwb);                                      \
+  } while (0)
 #if QR_TRAIL_WIDE
   // 16 waves (4 per SIMD) for tall strips: one wave's V staging latency is
   // covered by the other waves' MFMAs.
@@ -809,16 +861,18 @@ hipError_t launch_apply(const float* V, int64_t sVb, int64_t ldv, float* C, int6
   if (nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || kv_last < 1 || kv_last > 16 ||
       r < 16 * (nblk - 1) + kv_last)
     return hipErrorInvalidValue;
-  const int64_t wgs = (int64_t)((ncols + 15) / 16) * batch;
-  if (wgs > INT32_MAX) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)wgs);
-#define QR_APPLY_CASE(NWV, RLV)                                                                \
-  if (trans)                                                                                 \
-    hipLaunchKernelGGL((k_apply<NWV, RLV, true>), grid, dim3(64 * NWV), 0, stream, V, sVb, ldv, \
-                       C, sCb, ldc, nblk, r, ncols, Tws, sTwb, kv_last);                     \
-  else                                                                                       \
-    hipLaunchKernelGGL((k_apply<NWV, RLV, false>), grid, dim3(64 * NWV), 0, stream, V, sVb,   \
-                       ldv, C, sCb, ldc, nblk, r, ncols, Tws, sTwb, kv_last)
+  if ((int64_t)((ncols + 15) / 16) * batch > INT32_MAX) return hipErrorInvalidValue;
+#define QR_APPLY_CASE(NWV, RLV)                                                                 \
+  do {                                                                                          \
+    constexpr int KS = TrailKS<NWV, RLV>::value;                                                \
+    const dim3 grid((unsigned)((ncols + 16 * KS - 1) / (16 * KS) * (int64_t)batch));           \
+    if (trans)                                                                                  \
+      hipLaunchKernelGGL((k_apply<NWV, RLV, KS, true>), grid, dim3(64 * NWV), 0, stream, V,    \
+                         sVb, ldv, C, sCb, ldc, nblk, r, ncols, Tws, sTwb, kv_last);            \
+    else                                                                                        \
+      hipLaunchKernelGGL((k_apply<NWV, RLV, KS, false>), grid, dim3(64 * NWV), 0, stream, V,   \
+                         sVb, ldv, C, sCb, ldc, nblk, r, ncols, Tws, sTwb, kv_last);            \
+  } while (0)
   QR_STRIP_DISPATCH(r, QR_APPLY_CASE)
 #undef QR_APPLY_CASE
   return hipGetLastError();
