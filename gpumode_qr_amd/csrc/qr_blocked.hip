@@ -803,7 +803,7 @@ constexpr int kMaxStripRows = 4096;
 #define QR_TRAIL_WIDE 1
 #endif
 #ifndef QR_TRAIL_WIDE_MIN_ROWS
-#define QR_TRAIL_WIDE_MIN_ROWS 512
+#define QR_TRAIL_WIDE_MIN_ROWS 256
 #endif
 constexpr int kTrailWideMinRows = QR_TRAIL_WIDE_MIN_ROWS;
 constexpr int kMaxBlocks = 8;
@@ -836,8 +836,9 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
                        J0, nblk, r, c0, ncols, Tws, sTwb);                                      \
   } while (0)
 #if QR_TRAIL_WIDE
-  // 16 waves (4 per SIMD) for tall strips: one wave's V staging latency is
-  // covered by the other waves' MFMAs.
+  // 16 waves for strips of more than 256 rows: one wave's V staging latency is
+  // covered by the other waves' MFMAs (up to 1024 rows with two strips per
+  // workgroup, two workgroups per CU at 257-512 rows).
   if (r > kTrailWideMinRows && r <= 512) {
     QR_TRAIL_CASE(16, 8);
   } else if (r > 512 && r <= 1024) {
