@@ -58,9 +58,9 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 # x1.000). Counters cannot be read from inside this process; rerun those
 # commands after changing a kernel.
 HBM_MIB_PER_CALL = {
-    "smalln": {2: 33.0 + 33.2},
-    "panel": {3: 1260.6 + 381.3, 4: 429.4 + 140.2, 5: 446.0 + 134.1},
-    "trail": {3: 2362.8 + 1684.6, 4: 1657.0 + 1360.3, 5: 3253.7 + 2741.7},
+    "smalln": {2: 33.0 + 33.3},
+    "panel": {3: 1507.4 + 381.3, 4: 443.9 + 140.2, 5: 487.6 + 134.1},
+    "trail": {3: 2468.2 + 1690.0, 4: 1815.9 + 1473.6, 5: 3267.2 + 2809.1},
     "copy": {3: 640.0 + 640.0, 4: 256.0 + 256.0, 5: 256.0 + 256.0},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
