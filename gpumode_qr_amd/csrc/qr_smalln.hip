@@ -26,6 +26,9 @@
 namespace qr {
 
 constexpr int kSnWaves = 4;     // matrices (one per wave) per workgroup
+#ifndef QR_SMALLN_SIGMA_FROM_DS
+#define QR_SMALLN_SIGMA_FROM_DS 1
+#endif
 constexpr int kSnVStride = 20;  // row stride of the V transpose buffer (floats)
 
 template <int S>
@@ -131,29 +134,43 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   if constexpr (JJ > 0) smalln_t_column<S, JJ - 1>(col, sh, k);
 
   // x = column j below the diagonal (rows <= j masked), broadcast from lane JJ
-  // of every 16-lane row; partial dot with this lane's column.
-  float xb[NT][4];
+  // of every 16-lane row; partial dot with this lane's column. Rows <= j all
+  // lie in tile 0: its masked broadcast is kept for the update. The fast pass
+  // reads tiles 1.. straight from lane JJ's registers with the broadcast fused
+  // into v_fmac (dot4_bcast16 / axpy4_bcast16); the safe pass keeps them all.
+  constexpr int NX = kSafe ? NT : 1;
+  float xb[NX][4];
   float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < NT; ++t) {
+    if (!kSafe && t >= 1) {
+      dot4_bcast16<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
+                       c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3]);
+      continue;
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float own = c[P][4 * (P + t) + v];
       if (t == 0) own = (g >= (JJ - v + 4) / 4) ? own : 0.0f;  // row 4 g + v > JJ
-      xb[t][v] = row_bcast16<JJ>(own);
-      dv[v] = fmaf(xb[t][v], c[P][4 * (P + t) + v], dv[v]);
+      xb[t < NX ? t : 0][v] = row_bcast16<JJ>(own);
+      dv[v] = fmaf(xb[t < NX ? t : 0][v], c[P][4 * (P + t) + v], dv[v]);
     }
+  }
   // sigma and alpha, on the per-column critical path, come straight from the
   // four partial dots of lane JJ's row groups and from the lane that holds row
   // j; the per-lane sums over the row groups (needed by every column's update)
   // run beside them.
   const float dsum = (dv[0] + dv[1]) + (dv[2] + dv[3]);
-  const float sigma = (readlane_f(dsum, JJ) + readlane_f(dsum, JJ + 32)) +
-                      (readlane_f(dsum, JJ + 16) + readlane_f(dsum, JJ + 48));
   const float alpha = readlane_f(c[P][4 * P + vj], JJ + 16 * gj);
   const float ev = (g == gj) ? c[P][4 * P + vj] : 0.0f;  // row j of this column
   const float ds = rows16_sum(dsum);
   const float e = rows16_sum(ev);
+#if QR_SMALLN_SIGMA_FROM_DS
+  const float sigma = readlane_f(ds, JJ);  // lane JJ's dot is x^T x
+#else
+  const float sigma = (readlane_f(dsum, JJ) + readlane_f(dsum, JJ + 32)) +
+                      (readlane_f(dsum, JJ + 16) + readlane_f(dsum, JJ + 48));
+#endif
   // No rows below the diagonal (the last column): tau = 0. (Kept a runtime
   // test even when n = 16 S is known: the per-step branches keep the
   // scheduler from hoisting work across steps and raising register pressure.)
@@ -168,12 +185,15 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     // v^T c_k = c_k[j] + gamma x^T c_k;  c_k -= tau (v^T c_k) v.
     wk = fmaf(R.gamma, ds, e);
     const float cc = R.tau * wk;
-    const float cx = upd ? cc * R.gamma : 0.0f;
+    const float ncx = upd ? -(cc * R.gamma) : 0.0f;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int v = 0; v < 4; ++v) c[P][4 * P + v] = fmaf(ncx, xb[0][v], c[P][4 * P + v]);
+    // Tiles 1..: lane JJ (ncx = 0) is never changed, so each broadcast still
+    // reads column j's x.
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        c[P][4 * (P + t) + v] = fmaf(-cx, xb[t][v], c[P][4 * (P + t) + v]);
+    for (int t = 1; t < NT; ++t)
+      axpy4_bcast16<JJ>(c[P][4 * (P + t)], c[P][4 * (P + t) + 1], c[P][4 * (P + t) + 2],
+                        c[P][4 * (P + t) + 3], ncx);
     if (upd && g == gj) c[P][4 * P + vj] -= cc;
   } else {
     bool fast = true;
