@@ -298,6 +298,45 @@ def test_input_not_modified_and_repeatable():
     assert torch.equal(H1, H2) and torch.equal(t1, t2)
 
 
+@pytest.mark.parametrize("n,cols", [(100, (5, 37, 70)), (300, (20, 150, 290))])
+@pytest.mark.parametrize("scale", [1e-30, 1e25, 1e-40], ids=["tiny", "huge", "denormal"])
+def test_blocked_extreme_columns_vs_oracle(oracle, n, cols, scale):
+    """Columns far outside the fast reflector's range (sigma under 2^-100, over
+    2^100, or underflowing to zero) in the first panel and in later panels with
+    left-looking updates: the panel's fast pass hands them to the general pass,
+    whose slarfg scaling the oracle restates (oracle/qr_oracle.c)."""
+    _say(f"extreme columns n={n} cols={cols} scale={scale:g}")
+    A = _gauss(2, n, seed=n + 7)
+    A[0, :, cols[0]] *= scale
+    A[1, :, cols[1]] *= scale
+    A[1, :, cols[2]] *= scale
+    H, tau = _run(A)
+    assert torch.isfinite(H).all() and torch.isfinite(tau).all()
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"n={n} x{scale:g}")
+
+
+def test_side_stream_and_strided_input_bitwise():
+    """The call runs on the caller's current stream (a non-default one here), and
+    a transposed (column-major) input takes the same kernels after the strided
+    copy: both give the contiguous, default-stream result bit for bit."""
+    _say("side stream + transposed input (n=300)")
+    A = _gauss(3, 300, seed=21).to(DEV)
+    H0, t0 = hip_qr.geqrf(A)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        H1, t1 = hip_qr.geqrf(A)
+    torch.cuda.current_stream().wait_stream(side)
+    At = A.transpose(1, 2).contiguous().transpose(1, 2)  # same values, strides (n^2, 1, n)
+    assert At.stride() == (300 * 300, 1, 300) and torch.equal(At, A)
+    H2, t2 = hip_qr.geqrf(At)
+    torch.cuda.synchronize()
+    assert torch.equal(H0, H1) and torch.equal(t0, t1)
+    assert torch.equal(H0, H2) and torch.equal(t0, t2)
+
+
 @pytest.mark.parametrize("n,batch", [(300, 3), (1100, 2)])
 def test_lookahead_schedule_is_bitwise_identical(monkeypatch, n, batch):
     # The look-ahead schedule only splits the trailing update into disjoint
