@@ -188,13 +188,22 @@ hipError_t run_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r
   });
 }
 
-// Second stream (default priority) and two events per device for the
+// Second stream (default priority) and three events per device for the
 // look-ahead schedule of qr_geqrf_f32; created on first use, kept for the
 // life of the process.
+//
+// panels_done and rest_done only order kernels of two streams of one device,
+// and every kernel dispatch already acquires and releases at device scope, so
+// they are created without the system-scope fence (that fence writes caches
+// back for the host at every record: about 1 % of cfgs 3-5). all_done hands
+// the last side-stream update back to the caller's stream and keeps the
+// system-scope fence, so what the caller's stream completes is visible as
+// after any other kernel.
 struct Lookahead {
   hipStream_t s2 = nullptr;
   hipEvent_t panels_done = nullptr;
   hipEvent_t rest_done = nullptr;
+  hipEvent_t all_done = nullptr;
 };
 
 std::mutex g_la_mu;
@@ -209,15 +218,20 @@ bool lookahead_for_current_device(Lookahead* out) {
   if (!la.s2) {
     hipStream_t st = nullptr;
     if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return false;
-    hipEvent_t a = nullptr, b = nullptr;
-    if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
+    hipEvent_t a = nullptr, b = nullptr, c = nullptr;
+    const unsigned local = hipEventDisableTiming | hipEventDisableSystemFence;
+    if (hipEventCreateWithFlags(&a, local) != hipSuccess ||
+        hipEventCreateWithFlags(&b, local) != hipSuccess ||
+        hipEventCreateWithFlags(&c, hipEventDisableTiming) != hipSuccess) {
+      if (a) hipEventDestroy(a);
+      if (b) hipEventDestroy(b);
       hipStreamDestroy(st);
       return false;
     }
     la.s2 = st;
     la.panels_done = a;
     la.rest_done = b;
+    la.all_done = c;
   }
   *out = la;
   return true;
@@ -288,10 +302,12 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   // the update of every column right of block k+1, which runs concurrently
   // with the panels of block k+1. Events order the two streams:
   //   s2 waits for "panels of block k done" before updating with them;
-  //   s waits for "rest of block k done" before touching columns >= J0 + 2 NB.
+  //   s waits for "rest of block k done" before touching columns >= J0 + 2 NB;
+  //   at the end s waits for everything s2 did ("all done").
   Lookahead la;
   const bool use_la = lookahead_enabled() && n > 2 * NB && lookahead_for_current_device(&la);
   bool rest_pending = false;  // s2 holds work that s must wait for
+  bool s2_used = false;
 
   int blk = 0;
   for (int J0 = 0; J0 < n; J0 += NB, ++blk) {
@@ -325,11 +341,16 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
       if (e != hipSuccess) return QR_ELAUNCH;
       if (hipEventRecord(la.rest_done, la.s2) != hipSuccess) return QR_ELAUNCH;
       rest_pending = true;
+      s2_used = true;
     }
     e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, next, Tws, kTStride, batch, s);
     if (e != hipSuccess) return QR_ELAUNCH;
   }
-  if (rest_pending && hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;
+  if (s2_used) {
+    if (hipEventRecord(la.all_done, la.s2) != hipSuccess ||
+        hipStreamWaitEvent(s, la.all_done, 0) != hipSuccess)
+      return QR_ELAUNCH;
+  }
   return QR_OK;
 }
 
