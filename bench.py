@@ -53,10 +53,11 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
 # Measured HBM MiB (read + write) per geqrf call of each kernel family, per
 # config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
-# ``python -m gpumode_qr_amd.profile_run --config C --calls 3``, each scaled by
-# the same counter's reading for k_copy_in of known size (FETCH x2.000, WRITE
-# x1.000). Counters cannot be read from inside this process; rerun those
-# commands after changing a kernel.
+# ``python -m gpumode_qr_amd.profile_run --config C --calls 3 --layout colmajor``,
+# each scaled by the same counter's reading for k_copy_in of known size (FETCH
+# x2.000, WRITE x1.000; the column-major view is what makes the copy run).
+# Counters cannot be read from inside this process; rerun those commands after
+# changing a kernel.
 HBM_MIB_PER_CALL = {
     "smalln": {2: 33.0 + 33.3},
     "panel": {3: 1507.4 + 381.3, 4: 443.9 + 140.2, 5: 487.6 + 134.1},

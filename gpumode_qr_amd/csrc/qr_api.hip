@@ -23,10 +23,11 @@ namespace qr {
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                                float* tau, int batch, int n, hipStream_t stream);
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
-                        float* tau, int64_t sTaub, float* Tws, int64_t sTwb, int batch,
-                        hipStream_t stream);
+                        float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
+                        int64_t sAb, int64_t lda, int batch, hipStream_t stream);
 hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
-                        int ncols, const float* Tws, int64_t sTwb, int batch, hipStream_t stream);
+                        int ncols, const float* Tws, int64_t sTwb, const float* A, int64_t sAb,
+                        int64_t lda, int batch, hipStream_t stream);
 hipError_t launch_copy_in(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                           int64_t sHb, int batch, int n, hipStream_t stream);
 hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
@@ -165,26 +166,30 @@ hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, flo
   });
 }
 
+// A (when not null): where the outer block's columns are read from instead of H
+// (row stride lda, unit column stride); the results still go to H.
 hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw, float* tau,
-                     int64_t sTaub, float* T, int64_t sTb, int batch, hipStream_t s) {
+                     int64_t sTaub, float* T, int64_t sTb, int batch, hipStream_t s,
+                     const float* A = nullptr, int64_t sAb = 0, int64_t lda = 0) {
   // left-looking MFMA work (panels 0..p-1) + the panel's own factorisation
   const double flops = (4.0 * r * kPanel * kPanel * p + panel_flops(r - 16 * p, kw)) * batch;
   const double bytes = (2.0 * r * kw + (double)r * kPanel * p + kw + kPanel * kPanel * (p + 1)) *
                        4.0 * batch;
   return traced(QR_KERNEL_PANEL, flops, bytes, s, [&] {
-    return qr::launch_panel(H, sHb, ldh, J0, p, r, kw, tau, sTaub, T, sTb, batch, s);
+    return qr::launch_panel(H, sHb, ldh, J0, p, r, kw, tau, sTaub, T, sTb, A, sAb, lda, batch, s);
   });
 }
 
 // Columns c0 .. c0+ncols-1 (relative to the outer block at J0) := Q^T C.
 hipError_t run_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
-                     int ncols, const float* T, int64_t sTb, int batch, hipStream_t s) {
+                     int ncols, const float* T, int64_t sTb, int batch, hipStream_t s,
+                     const float* A = nullptr, int64_t sAb = 0, int64_t lda = 0) {
   double rows = 0.0;  // sum over the blocks of their row counts
   for (int q = 0; q < nblk; ++q) rows += r - kPanel * q;
   const double flops = 4.0 * kPanel * (double)ncols * rows * batch;
   const double bytes = (2.0 * r * ncols + rows * kPanel) * 4.0 * batch;
   return traced(QR_KERNEL_TRAIL, flops, bytes, s, [&] {
-    return qr::launch_trail(H, sHb, ldh, J0, nblk, r, c0, ncols, T, sTb, batch, s);
+    return qr::launch_trail(H, sHb, ldh, J0, nblk, r, c0, ncols, T, sTb, A, sAb, lda, batch, s);
   });
 }
 
@@ -290,10 +295,17 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   float* Tslot[2] = {static_cast<float*>(workspace),
                      static_cast<float*>(workspace) + (size_t)batch * kTStride};
 
-  hipError_t e = traced(QR_KERNEL_COPY, 0.0, 2.0 * nn * 4.0 * batch, s, [&] {
-    return qr::launch_copy_in(A, sAb, sAr, sAc, H, nn, batch, n, s);
-  });
-  if (e != hipSuccess) return QR_ELAUNCH;
+  // With a unit column stride the first outer block reads A itself: its panels
+  // and trailing updates write every element of H, so no copy is needed.
+  // Other layouts (e.g. a transposed view) are copied into H first.
+  const bool direct = sAc == 1;
+  hipError_t e = hipSuccess;
+  if (!direct) {
+    e = traced(QR_KERNEL_COPY, 0.0, 2.0 * nn * 4.0 * batch, s, [&] {
+      return qr::launch_copy_in(A, sAb, sAr, sAc, H, nn, batch, n, s);
+    });
+    if (e != hipSuccess) return QR_ELAUNCH;
+  }
   const int P = outer_blocks(n);
   const int NB = kPanel * P;
 
@@ -312,17 +324,19 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   int blk = 0;
   for (int J0 = 0; J0 < n; J0 += NB, ++blk) {
     float* Tws = Tslot[blk & 1];
+    const float* Ab = (direct && J0 == 0) ? A : nullptr;  // source of this block's columns
     const int r = n - J0;
     const int nblk = (r + kPanel - 1) / kPanel < P ? (r + kPanel - 1) / kPanel : P;
     for (int p = 0; p < nblk; ++p) {
       const int kw = (r - kPanel * p) < kPanel ? (r - kPanel * p) : kPanel;
-      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s);
+      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s, Ab, sAb, sAr);
       if (e != hipSuccess) return QR_ELAUNCH;
     }
     const int ncols = r - kPanel * nblk;
     if (ncols <= 0) continue;
     if (!use_la) {
-      e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, ncols, Tws, kTStride, batch, s);
+      e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, ncols, Tws, kTStride, batch, s, Ab, sAb,
+                    sAr);
       if (e != hipSuccess) return QR_ELAUNCH;
       continue;
     }
@@ -337,13 +351,14 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
       if (hipEventRecord(la.panels_done, s) != hipSuccess) return QR_ELAUNCH;
       if (hipStreamWaitEvent(la.s2, la.panels_done, 0) != hipSuccess) return QR_ELAUNCH;
       e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk + next, rest, Tws, kTStride, batch,
-                    la.s2);
+                    la.s2, Ab, sAb, sAr);
       if (e != hipSuccess) return QR_ELAUNCH;
       if (hipEventRecord(la.rest_done, la.s2) != hipSuccess) return QR_ELAUNCH;
       rest_pending = true;
       s2_used = true;
     }
-    e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, next, Tws, kTStride, batch, s);
+    e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, next, Tws, kTStride, batch, s, Ab, sAb,
+                  sAr);
     if (e != hipSuccess) return QR_ELAUNCH;
   }
   if (s2_used) {

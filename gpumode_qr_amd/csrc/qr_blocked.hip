@@ -260,17 +260,19 @@ __device__ __forceinline__ void panel_general_pass(float (&c)[RL], PanelShared<N
   }
 }
 
-// c := panel p (kw columns at Blk + 16 p, r rows, strip layout) after the
-// left-looking update with panels 0..p-1 of the outer block at Blk.
+// c := panel p (kw columns at Src + 16 p, row stride lds, r rows, strip
+// layout) after the left-looking update with panels 0..p-1 of the outer block
+// at Blk (V and R in place, row stride ldh).
 template <int NW, int RL>
 __device__ __forceinline__ void panel_load_apply(float (&c)[1][RL], const float* __restrict__ Blk,
-                                                 int64_t ldh, int p, int r, int kw,
+                                                 int64_t ldh, const float* Src, int64_t lds,
+                                                 int p, int r, int kw,
                                                  const float* __restrict__ Tb,
                                                  WyPipeShared<NW, RL>& wy, int w, int lane) {
   auto block = [&](int q) { return VBlock{Blk + (int64_t)(16 * q) * ldh + 16 * q, 16 * q, 16}; };
   VChunk<NW, RL> ck;
   if (p > 0) load_v_chunk<NW, RL>(ck, block(0), ldh, r, 0, w, lane);
-  load_strip<NW, RL>(c[0], Blk + 16 * p, ldh, r, kw, w, lane);
+  load_strip<NW, RL>(c[0], Src + 16 * p, lds, r, kw, w, lane);
   for (int q = 0; q < p; ++q)
     apply_wy16p<NW, RL, 1>(c, ck, block(q), Tb + 256 * q, block(q + 1 < p ? q + 1 : q), q + 1 < p,
                            ldh, r, wy, w, lane);
@@ -284,12 +286,15 @@ constexpr bool kPanelFastPass = QR_PANEL_FAST != 0;
 
 // Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
 // Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
-// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p.
+// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p. The panel's columns are
+// read from H, or from A (row stride lda, unit column stride) when A is not
+// null: the first outer block reads the caller's matrix directly.
 template <int NW, int RL>
 __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
                                                    int64_t ldh, int J0, int p, int r, int kw,
                                                    float* __restrict__ tau, int64_t sTaub,
-                                                   float* __restrict__ Tws, int64_t sTwb) {
+                                                   float* __restrict__ Tws, int64_t sTwb,
+                                                   const float* A, int64_t sAb, int64_t lda) {
   using S = Strip<NW, RL>;
   __shared__ PanelShared<NW, RL> sh;
 
@@ -300,12 +305,14 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
   float* P = Blk + 16 * p;
   float* Tb = Tws + (int64_t)b * sTwb;
+  const float* Src = A ? A + (int64_t)b * sAb + (int64_t)J0 * lda + J0 : Blk;
+  const int64_t lds = A ? lda : ldh;
 
   // The panel after the left-looking update with panels 0..p-1; the panel in
   // HBM is not written before the end, so the general pass can start over.
   float cs[1][RL];
   float (&c)[RL] = cs[0];
-  panel_load_apply<NW, RL>(cs, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
+  panel_load_apply<NW, RL>(cs, Blk, ldh, Src, lds, p, r, kw, Tb, sh.wy, w, lane);
 
   PanelCol st;
   bool ok = false;
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   if (!ok) [[unlikely]] {
     if constexpr (kPanelFastPass) {
       __syncthreads();  // every wave is past its last read of erow / red
-      panel_load_apply<NW, RL>(cs, Blk, ldh, p, r, kw, Tb, sh.wy, w, lane);
+      panel_load_apply<NW, RL>(cs, Blk, ldh, Src, lds, p, r, kw, Tb, sh.wy, w, lane);
       st = PanelCol{};
     }
     panel_general_pass<NW, RL>(c, sh, p, r, kw, w, lane, st);
@@ -372,14 +379,16 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
 
 // Columns c0.. c0+ncols-1 (relative to the outer block at J0, r rows) :=
 // Q^T C with the nblk 16-wide reflector blocks of the outer block, applied
-// in order 0..nblk-1. Each workgroup updates KS adjacent 16-column strips;
+// in order 0..nblk-1. C is read from H, or from A (row stride lda, unit column
+// stride) when A is not null, and written to H. Each workgroup updates KS adjacent 16-column strips;
 // 1-D grid of ngroups * batch workgroups, ngroups = ceil(ncols / (16 KS)),
 // group-major within a matrix after the XCD renumbering.
 template <int NW, int RL, int KS>
 __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_t sHb,
                                                    int64_t ldh, int J0, int nblk, int r, int c0,
                                                    int ncols, const float* __restrict__ Tws,
-                                                   int64_t sTwb) {
+                                                   int64_t sTwb, const float* A, int64_t sAb,
+                                                   int64_t lda) {
   __shared__ WyPipeShared<NW, RL, KS> wy;
   const int ngroups = (ncols + 16 * KS - 1) / (16 * KS);
   const int id = xcd_logical_id(blockIdx.x, gridDim.x);
@@ -389,6 +398,8 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   float* Blk = H + (int64_t)b * sHb + (int64_t)J0 * ldh + J0;
   const int s0 = 16 * KS * (id - b * ngroups);
   float* P = Blk + c0 + s0;
+  const float* Ps = (A ? A + (int64_t)b * sAb + (int64_t)J0 * lda + J0 : Blk) + c0 + s0;
+  const int64_t lds = A ? lda : ldh;
   const float* Tb = Tws + (int64_t)b * sTwb;
   auto block = [&](int q) { return VBlock{Blk + (int64_t)(16 * q) * ldh + 16 * q, 16 * q, 16}; };
   // Columns of strip st inside the matrix (<= 0: strip past the last column).
@@ -400,7 +411,7 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
   float c[KS][RL];
   VChunk<NW, RL> ck;
 #pragma unroll
-  for (int st = 0; st < KS; ++st) load_strip<NW, RL>(c[st], P + 16 * st, ldh, r, ncol(st), w, lane);
+  for (int st = 0; st < KS; ++st) load_strip<NW, RL>(c[st], Ps + 16 * st, lds, r, ncol(st), w, lane);
   // The strip's loads are issued (and their 64-bit addresses dead) before the
   // first V chunk's: the compiler would otherwise keep every address live at
   // once and spill.
@@ -415,21 +426,21 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
 }
 
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
-                        float* tau, int64_t sTaub, float* Tws, int64_t sTwb, int batch,
-                        hipStream_t stream) {
+                        float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
+                        int64_t sAb, int64_t lda, int batch, hipStream_t stream) {
   if (kw < 1 || kw > 16 || p < 0 || p >= kMaxBlocks || r > kMaxStripRows || r < 16 * p + kw)
     return hipErrorInvalidValue;
 #define QR_PANEL_CASE(NWV, RLV)                                                             \
   hipLaunchKernelGGL((k_panel<NWV, RLV>), dim3(batch), dim3(64 * NWV), 0, stream, H, sHb, ldh, \
-                     J0, p, r, kw, tau, sTaub, Tws, sTwb)
+                     J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda)
   QR_STRIP_DISPATCH(r, QR_PANEL_CASE)
 #undef QR_PANEL_CASE
   return hipGetLastError();
 }
 
 hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
-                        int ncols, const float* Tws, int64_t sTwb, int batch,
-                        hipStream_t stream) {
+                        int ncols, const float* Tws, int64_t sTwb, const float* A, int64_t sAb,
+                        int64_t lda, int batch, hipStream_t stream) {
   if (ncols <= 0) return hipSuccess;
   if (nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || r < 16 * (nblk - 1) + 1)
     return hipErrorInvalidValue;
@@ -439,7 +450,7 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
     constexpr int KS = TrailKS<NWV, RLV>::value;                                                \
     const dim3 grid((unsigned)((ncols + 16 * KS - 1) / (16 * KS) * (int64_t)batch));           \
     hipLaunchKernelGGL((k_trail<NWV, RLV, KS>), grid, dim3(64 * NWV), 0, stream, H, sHb, ldh,  \
-                       J0, nblk, r, c0, ncols, Tws, sTwb);                                      \
+                       J0, nblk, r, c0, ncols, Tws, sTwb, A, sAb, lda);                         \
   } while (0)
 #if QR_TRAIL_WIDE
   // 16 waves for strips of more than 256 rows: one wave's V staging latency is

@@ -6,8 +6,12 @@ Unlike ``bench.py`` this runs no FP64 gates (they call torch's
 householder_product) and no torch.geqrf, so a ``rocprofv3 --pmc`` pass over it
 sees the library's own kernels and nothing else. Every call of ``geqrf``
 launches the same kernels, so per-dispatch counters divide cleanly by call.
-``k_copy_in`` reads ``batch * n * n * 4`` bytes and writes as many: it is the
-known-size copy that calibrates FETCH_SIZE / WRITE_SIZE.
+
+``--layout colmajor`` passes the same matrices as a column-major view. A
+matrix without a unit column stride is first copied into H by ``k_copy_in``,
+which reads ``batch * n * n * 4`` bytes and writes as many: the known-size
+copy that calibrates FETCH_SIZE / WRITE_SIZE. The other kernels move the same
+bytes in both layouts (the first outer block reads A instead of H).
 """
 
 from __future__ import annotations
@@ -20,6 +24,8 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", type=int, default=4, help="1..5 (the benchmark configs)")
     ap.add_argument("--calls", type=int, default=3)
+    ap.add_argument("--layout", choices=("rowmajor", "colmajor"), default="rowmajor",
+                    help="colmajor: a column-major view of the same matrices (adds k_copy_in)")
     args = ap.parse_args(argv)
 
     import torch
@@ -32,10 +38,13 @@ def main(argv=None) -> int:
     _lib.load()
     prob = inputs.make_config_problem(args.config, device="cuda")
     A = prob.tensor
+    if args.layout == "colmajor":
+        A = A.transpose(-1, -2).contiguous().transpose(-1, -2)
     b, n = prob.batch, prob.n
     ws = torch.empty(max(1, hip_qr.workspace_bytes(b, n)), dtype=torch.uint8, device="cuda")
-    print(f"[profile_run] {prob.name}: batch={b} n={n}, copy-in bytes per call "
-          f"{b * n * n * 4} read + {b * n * n * 4} written", flush=True)
+    print(f"[profile_run] {prob.name}: batch={b} n={n} layout={args.layout}, copy-in bytes "
+          f"per call {b * n * n * 4 if args.layout == 'colmajor' and n > 64 else 0} read and "
+          f"as many written", flush=True)
     for i in range(args.calls):
         hip_qr.geqrf(A, workspace=ws)
         torch.cuda.synchronize()

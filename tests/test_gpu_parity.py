@@ -337,6 +337,28 @@ def test_side_stream_and_strided_input_bitwise():
     assert torch.equal(H0, H2) and torch.equal(t0, t2)
 
 
+@pytest.mark.parametrize("lookahead", ["1", "0"])
+@pytest.mark.parametrize("n", [100, 700, 1100])
+def test_first_block_reads_padded_input_directly(monkeypatch, n, lookahead):
+    """Input with a unit column stride but padded rows and batch (row stride
+    n + 7, batch stride (n + 3) (n + 7)) is read in place by the first outer
+    block's kernels; a column-major view of the same values goes through the
+    strided copy first. Both give the same bits, with and without look-ahead."""
+    monkeypatch.setenv("QR_LOOKAHEAD", lookahead)
+    _say(f"padded input read directly (n={n}, lookahead={lookahead})")
+    batch = 2
+    base = torch.randn(batch, n + 3, n + 7, generator=torch.Generator().manual_seed(n))
+    Ap = base.to(DEV)[:, 1:n + 1, 2:n + 2]
+    assert Ap.stride() == ((n + 3) * (n + 7), n + 7, 1)
+    Ac = Ap.transpose(1, 2).contiguous().transpose(1, 2)
+    assert Ac.stride(2) == n and torch.equal(Ac, Ap)
+    Hp, tp = hip_qr.geqrf(Ap)
+    Hc, tc = hip_qr.geqrf(Ac)
+    torch.cuda.synchronize()
+    assert torch.equal(Hp, Hc) and torch.equal(tp, tc)
+    assert torch.equal(Ap, Ac)  # the input is left as it was
+
+
 @pytest.mark.parametrize("n,batch", [(300, 3), (1100, 2)])
 def test_lookahead_schedule_is_bitwise_identical(monkeypatch, n, batch):
     # The look-ahead schedule only splits the trailing update into disjoint
