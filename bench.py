@@ -53,16 +53,14 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
 # Measured HBM MiB (read + write) per geqrf call of each kernel family, per
 # config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
-# ``python -m gpumode_qr_amd.profile_run --config C --calls 3 --layout colmajor``,
-# each scaled by the same counter's reading for k_copy_in of known size (FETCH
-# x2.000, WRITE x1.000; the column-major view is what makes the copy run).
-# Counters cannot be read from inside this process; rerun those commands after
-# changing a kernel.
+# ``python -m gpumode_qr_amd.profile_run --config C --calls 3``, each scaled by
+# the same counter's reading for a known-size elementwise kernel that
+# profile_run runs first (FETCH x2.000, WRITE x1.000). Counters cannot be read
+# from inside this process; rerun those commands after changing a kernel.
 HBM_MIB_PER_CALL = {
-    "smalln": {2: 33.0 + 33.3},
-    "panel": {3: 1507.4 + 381.3, 4: 443.9 + 140.2, 5: 487.6 + 134.1},
-    "trail": {3: 2468.2 + 1690.0, 4: 1815.9 + 1473.6, 5: 3267.2 + 2809.1},
-    "copy": {3: 640.0 + 640.0, 4: 256.0 + 256.0, 5: 256.0 + 256.0},
+    "smalln": {2: 32.9 + 32.7},
+    "panel": {3: 1531.3 + 381.3, 4: 459.9 + 140.2, 5: 495.5 + 134.1},
+    "trail": {3: 2488.6 + 1697.6, 4: 1819.2 + 1446.3, 5: 3265.2 + 2807.1},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 

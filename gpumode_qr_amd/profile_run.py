@@ -7,11 +7,13 @@ householder_product) and no torch.geqrf, so a ``rocprofv3 --pmc`` pass over it
 sees the library's own kernels and nothing else. Every call of ``geqrf``
 launches the same kernels, so per-dispatch counters divide cleanly by call.
 
-``--layout colmajor`` passes the same matrices as a column-major view. A
-matrix without a unit column stride is first copied into H by ``k_copy_in``,
-which reads ``batch * n * n * 4`` bytes and writes as many: the known-size
-copy that calibrates FETCH_SIZE / WRITE_SIZE. The other kernels move the same
-bytes in both layouts (the first outer block reads A instead of H).
+Before the calls it runs one ``torch.neg(A, out=C)``: an elementwise kernel
+that reads ``batch * n * n * 4`` bytes and writes as many, the known-size
+transfer that calibrates FETCH_SIZE / WRITE_SIZE.
+
+``--layout colmajor`` passes the same matrices as a column-major view, which
+geqrf first copies into H with ``k_copy_in`` (with the row-major default the
+first outer block reads A in place and there is no copy).
 """
 
 from __future__ import annotations
@@ -42,9 +44,12 @@ def main(argv=None) -> int:
         A = A.transpose(-1, -2).contiguous().transpose(-1, -2)
     b, n = prob.batch, prob.n
     ws = torch.empty(max(1, hip_qr.workspace_bytes(b, n)), dtype=torch.uint8, device="cuda")
-    print(f"[profile_run] {prob.name}: batch={b} n={n} layout={args.layout}, copy-in bytes "
-          f"per call {b * n * n * 4 if args.layout == 'colmajor' and n > 64 else 0} read and "
-          f"as many written", flush=True)
+    print(f"[profile_run] {prob.name}: batch={b} n={n} layout={args.layout}; calibration "
+          f"kernel (neg) reads {b * n * n * 4} bytes and writes as many", flush=True)
+    C = torch.empty_like(A)
+    torch.neg(A, out=C)  # calibration: b n^2 4 bytes read, as many written
+    torch.cuda.synchronize()
+    del C
     for i in range(args.calls):
         hip_qr.geqrf(A, workspace=ws)
         torch.cuda.synchronize()
