@@ -28,6 +28,7 @@ hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r
 hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
                         int ncols, const float* Tws, int64_t sTwb, const float* A, int64_t sAb,
                         int64_t lda, int batch, hipStream_t stream);
+hipError_t trail_grid(int r, int ncols, int batch, int64_t* wgs, int64_t* resident);
 hipError_t launch_copy_in(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                           int64_t sHb, int batch, int n, hipStream_t stream);
 hipError_t launch_larft(const float* V, int64_t sVb, int64_t ldv, int m, int k, const float* tau,
@@ -339,6 +340,24 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
                     sAr);
       if (e != hipSuccess) return QR_ELAUNCH;
       continue;
+    }
+    // When the whole update fits on the device in one round of workgroups, a
+    // split buys no overlap, only the cross-stream packets between the panels
+    // and the next update (about 10 us per block): one launch on s instead.
+    // Every strip's arithmetic is the same either way.
+    {
+      int64_t wgs = 0, resident = 1;
+      if (qr::trail_grid(r, ncols, batch, &wgs, &resident) != hipSuccess) return QR_ELAUNCH;
+      if (wgs <= resident) {
+        if (rest_pending) {
+          if (hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;
+          rest_pending = false;
+        }
+        e = run_trail(H, nn, n, J0, nblk, r, kPanel * nblk, ncols, Tws, kTStride, batch, s, Ab,
+                      sAb, sAr);
+        if (e != hipSuccess) return QR_ELAUNCH;
+        continue;
+      }
     }
     const int next = ncols < NB ? ncols : NB;
     const int rest = ncols - next;

@@ -472,4 +472,53 @@ hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, in
   return hipGetLastError();
 }
 
+// Workgroups launch_trail would launch for (r, ncols, batch), and how many of
+// them the device holds at once (occupancy of that kernel instance times the
+// CU count; cached per instance).
+hipError_t trail_grid(int r, int ncols, int batch, int64_t* wgs, int64_t* resident) {
+  *wgs = 0;
+  *resident = 1;
+  if (ncols <= 0 || r > kMaxStripRows) return hipSuccess;
+  static std::atomic<int> per_cu[16];
+  int slot = 0;
+  hipError_t e = hipSuccess;
+#define QR_TRAIL_GRID_CASE(NWV, RLV)                                                         \
+  do {                                                                                       \
+    constexpr int KS = TrailKS<NWV, RLV>::value;                                             \
+    *wgs = (int64_t)((ncols + 16 * KS - 1) / (16 * KS)) * batch;                            \
+    int v = per_cu[slot].load(std::memory_order_relaxed);                                    \
+    if (v <= 0) {                                                                            \
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                      \
+          &v, reinterpret_cast<const void*>(&k_trail<NWV, RLV, KS>), 64 * NWV, 0);           \
+      if (e != hipSuccess) return e;                                                         \
+      if (v < 1) v = 1;                                                                      \
+      per_cu[slot].store(v, std::memory_order_relaxed);                                      \
+    }                                                                                        \
+    *resident = (int64_t)v * device_cu_count();                                              \
+  } while (0)
+#if QR_TRAIL_WIDE
+  if (r > kTrailWideMinRows && r <= 512) {
+    slot = 1;
+    QR_TRAIL_GRID_CASE(16, 8);
+  } else if (r > 512 && r <= 1024) {
+    slot = 2;
+    QR_TRAIL_GRID_CASE(16, 16);
+  } else if (r > 1024 && r <= 2048) {
+    slot = 3;
+    QR_TRAIL_GRID_CASE(16, 32);
+  } else
+#endif
+  {
+#define QR_TRAIL_GRID_CASE2(NWV, RLV)                                             \
+  do {                                                                            \
+    slot = 4 + (RLV >= 8) + (RLV >= 16) + (RLV >= 32) + (RLV >= 64) + (NWV == 16 ? 5 : 0); \
+    QR_TRAIL_GRID_CASE(NWV, RLV);                                                 \
+  } while (0)
+    QR_STRIP_DISPATCH(r, QR_TRAIL_GRID_CASE2)
+#undef QR_TRAIL_GRID_CASE2
+  }
+#undef QR_TRAIL_GRID_CASE
+  return e;
+}
+
 }  // namespace qr

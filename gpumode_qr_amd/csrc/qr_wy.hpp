@@ -12,6 +12,8 @@
 // src/qrbench/variants.py:800-804.
 #pragma once
 
+#include <atomic>
+
 #include "qr_device.hpp"
 
 namespace qr {
@@ -338,6 +340,22 @@ struct TrailKS {
   } else {                           \
     CASE(16, 64);                    \
   }
+
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+inline int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
 
 constexpr int kMaxStripRows = 4096;
 #ifndef QR_TRAIL_WIDE
