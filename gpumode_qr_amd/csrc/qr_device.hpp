@@ -184,6 +184,47 @@ __device__ __forceinline__ void axpy4_bcast16(float& x0, float& x1, float& x2, f
       : "v"(s), "i"(J));
 }
 
+// Row mask of the 16-lane rows g whose row 4 g + v of a 16-row tile lies below
+// row J (4 g + v > J): bit g enables lanes 16 g .. 16 g + 15.
+template <int J, int V>
+constexpr int rows_below_mask() {
+  return (0xF << ((J - V + 4) / 4)) & 0xF;
+}
+
+// dot4_bcast16 for the tile that holds row J: a_v += x_v[J] x_v only in the
+// rows below row J (rows_below_mask); the other rows keep a_v. DPP's row mask
+// gates the destination write, not the source read.
+template <int J>
+__device__ __forceinline__ void dot4_bcast16_below(float& a0, float& a1, float& a2, float& a3,
+                                                   float x0, float x1, float x2, float x3) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  asm("s_nop 4\n\t"
+      "v_fmac_f32_dpp %0, %4, %4 row_newbcast:%8 row_mask:%9 bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %5, %5 row_newbcast:%8 row_mask:%10 bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %2, %6, %6 row_newbcast:%8 row_mask:%11 bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %3, %7, %7 row_newbcast:%8 row_mask:%12 bank_mask:0xf bound_ctrl:1"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)
+      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J), "i"(rows_below_mask<J, 0>()),
+        "i"(rows_below_mask<J, 1>()), "i"(rows_below_mask<J, 2>()),
+        "i"(rows_below_mask<J, 3>()));
+}
+
+// axpy4_bcast16 for the tile that holds row J: x_v += x_v[J] s only in the rows
+// below row J.
+template <int J>
+__device__ __forceinline__ void axpy4_bcast16_below(float& x0, float& x1, float& x2, float& x3,
+                                                    float s) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  asm("s_nop 4\n\t"
+      "v_fmac_f32_dpp %0, %0, %4 row_newbcast:%5 row_mask:%6 bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %1, %4 row_newbcast:%5 row_mask:%7 bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %2, %2, %4 row_newbcast:%5 row_mask:%8 bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %3, %3, %4 row_newbcast:%5 row_mask:%9 bank_mask:0xf bound_ctrl:1"
+      : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+      : "v"(s), "i"(J), "i"(rows_below_mask<J, 0>()), "i"(rows_below_mask<J, 1>()),
+        "i"(rows_below_mask<J, 2>()), "i"(rows_below_mask<J, 3>()));
+}
+
 // Sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
 __device__ __forceinline__ float sum_over_rows16(float v) {
   v += __shfl_xor(v, 16);

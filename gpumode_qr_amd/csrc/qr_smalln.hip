@@ -138,14 +138,20 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   // lie in tile 0: its masked broadcast is kept for the update. The fast pass
   // reads tiles 1.. straight from lane JJ's registers with the broadcast fused
   // into v_fmac (dot4_bcast16 / axpy4_bcast16); the safe pass keeps them all.
+  // Fast pass: tile 0's rows at or above row JJ are left out by the DPP row
+  // mask of the fused broadcast (dot4_bcast16_below), not by selects.
   constexpr int NX = kSafe ? NT : 1;
   float xb[NX][4];
   float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    if (!kSafe && t >= 1) {
-      dot4_bcast16<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
-                       c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3]);
+    if constexpr (!kSafe) {
+      if (t == 0)
+        dot4_bcast16_below<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * P], c[P][4 * P + 1],
+                               c[P][4 * P + 2], c[P][4 * P + 3]);
+      else
+        dot4_bcast16<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
+                         c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3]);
       continue;
     }
 #pragma unroll
@@ -186,10 +192,9 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     wk = fmaf(R.gamma, ds, e);
     const float cc = R.tau * wk;
     const float ncx = upd ? -(cc * R.gamma) : 0.0f;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) c[P][4 * P + v] = fmaf(ncx, xb[0][v], c[P][4 * P + v]);
-    // Tiles 1..: lane JJ (ncx = 0) is never changed, so each broadcast still
-    // reads column j's x.
+    // Tile 0 below row JJ, then tiles 1..: lane JJ (ncx = 0) is never changed,
+    // so each broadcast still reads column j's x.
+    axpy4_bcast16_below<JJ>(c[P][4 * P], c[P][4 * P + 1], c[P][4 * P + 2], c[P][4 * P + 3], ncx);
 #pragma unroll
     for (int t = 1; t < NT; ++t)
       axpy4_bcast16<JJ>(c[P][4 * (P + t)], c[P][4 * (P + t) + 1], c[P][4 * (P + t) + 2],
