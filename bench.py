@@ -238,7 +238,7 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: the library has no multi-GPU path "
               "(the batch would shard across GPUs with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         return 2

@@ -36,7 +36,7 @@ BENCHMARK_SHAPES: list[dict] = [
     {"batch": 2, "cond": 1, "n": 4096},
 ]
 
-# The five headline configs of this build (name -> spec).
+# The five headline benchmark configs (name -> spec).
 CONFIGS: list[dict] = [
     {"cfg": 1, "name": "cfg1_b64_n32_gauss", "batch": 64, "n": 32, "kind": "gauss", "seed": 0},
     {"cfg": 2, "name": "cfg2_b2048_n64_gauss", "batch": 2048, "n": 64, "kind": "gauss", "seed": 2},

@@ -21,7 +21,7 @@
  *   qro_larfb_lt the trailing update of src/qrbench/variants.py:800-804
  *                (C -= V (T^T (V^T C))).
  *   qro_geqrf    the right-looking blocked loop of variants.py:786-805.
- *   qro_orgqr    Q = H_0 ... H_{n-1}, i.e. what the checker materialises with
+ *   qro_orgqr    Q = H_0 ... H_{n-1}, i.e. what the reference's gates build with
  *                torch.linalg.householder_product (src/qrbench/checker.py:129).
  *
  * Parity pins (tests/test_oracle.py): MKL sgeqrf via torch.geqrf on CPU and the

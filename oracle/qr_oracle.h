@@ -1,7 +1,8 @@
 /*
  * qr_oracle.h -- CPU restatement of batched compact-Householder QR (fp32),
- * used ONLY as a test checker (tests/, __graft_entry__.smoke(), bench.py's
- * cpu_baseline leg). It is never linked into, or called by, the product path.
+ * used ONLY by the tests, the smoke check and the CPU baseline (tests/,
+ * __graft_entry__.smoke(), bench.py's cpu_baseline leg). It is never linked
+ * into, or called by, the product path.
  *
  * Storage is row-major: element (i, j) of a matrix with row stride `ld`
  * lives at A[i * ld + j]. This is the layout torch uses for a contiguous
