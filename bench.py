@@ -59,8 +59,8 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 # from inside this process; rerun those commands after changing a kernel.
 HBM_MIB_PER_CALL = {
     "smalln": {2: 32.9 + 32.7},
-    "panel": {3: 1531.3 + 381.3, 4: 459.9 + 140.2, 5: 495.5 + 134.1},
-    "trail": {3: 2488.6 + 1697.6, 4: 1819.2 + 1446.3, 5: 3265.2 + 2807.1},
+    "panel": {3: 1547.0 + 381.3, 4: 459.9 + 140.2, 5: 495.5 + 134.1},
+    "trail": {3: 2487.1 + 1697.1, 4: 1803.7 + 1445.1, 5: 3254.4 + 2809.4},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
