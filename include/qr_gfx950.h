@@ -36,7 +36,7 @@ typedef enum qr_kernel_id {
   QR_KERNEL_SMALLN = 0, /* kernel (a) */
   QR_KERNEL_PANEL = 1,  /* kernel (b), incl. its left-looking block update */
   QR_KERNEL_TRAIL = 2,  /* kernel (d), trailing compact-WY update */
-  QR_KERNEL_COPY = 3,   /* strided A -> H copy */
+  QR_KERNEL_COPY = 3,   /* A -> H copy (only for A without a unit column stride) */
   QR_KERNEL_LARFT = 4,  /* kernel (c) */
   QR_KERNEL_APPLY = 5   /* block-reflector application of orgqr / ormqr */
 } qr_kernel_id;
@@ -57,7 +57,9 @@ size_t qr_geqrf_f32_workspace(int batch, int n);
  * Full factorisation, replacing the champion variant's forward pass
  * (reference src/qrbench/variants.py:876-917 -> :761-805 for n > 128 and
  * :698-758 for n <= 128; baseline torch.geqrf at src/qrbench/reference.py:18-20).
- * A: (batch, n, n) with element strides (sAb, sAr, sAc), read only.
+ * A: (batch, n, n) with element strides (sAb, sAr, sAc), read only. With
+ *    sAc == 1 the kernels read A in place; other layouts are first copied
+ *    into H.
  * H: contiguous (batch, n, n) output, R on and above the diagonal, essential
  *    Householder vectors below it. tau: contiguous (batch, n) output.
  * H must not overlap A.
