@@ -213,6 +213,11 @@ struct Lookahead {
 };
 
 std::mutex g_la_mu;
+// Held for the whole enqueue of a call that uses the second stream: the
+// stream and its events are shared by every call on the device, so two host
+// threads must not interleave their records and waits (a call's side-stream
+// wait could otherwise capture another call's "panels done").
+std::mutex g_la_call_mu;
 std::vector<Lookahead> g_la;
 
 bool lookahead_for_current_device(Lookahead* out) {
@@ -319,6 +324,8 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   //   at the end s waits for everything s2 did ("all done").
   Lookahead la;
   const bool use_la = lookahead_enabled() && n > 2 * NB && lookahead_for_current_device(&la);
+  std::unique_lock<std::mutex> la_lock(g_la_call_mu, std::defer_lock);
+  if (use_la) la_lock.lock();
   bool rest_pending = false;  // s2 holds work that s must wait for
   bool s2_used = false;
 

@@ -337,6 +337,45 @@ def test_side_stream_and_strided_input_bitwise():
     assert torch.equal(H0, H2) and torch.equal(t0, t2)
 
 
+def test_concurrent_host_threads_bitwise():
+    """Two host threads, each on its own stream, factor different matrices at
+    the same time. Both calls use the library's shared look-ahead stream
+    (n > 128). Every result equals the one of a lone call, bit for bit."""
+    import threading
+
+    _say("two host threads, two streams, shared look-ahead stream")
+    A1 = _gauss(3, 300, seed=5).to(DEV)
+    A2 = _gauss(8, 700, seed=6).to(DEV)
+    ref = {"a": hip_qr.geqrf(A1), "b": hip_qr.geqrf(A2)}
+    torch.cuda.synchronize()
+    results, errors = {}, []
+
+    def work(key, A):
+        try:
+            st = torch.cuda.Stream()
+            outs = []
+            with torch.cuda.stream(st):
+                for _ in range(6):
+                    outs.append(hip_qr.geqrf(A))
+            st.synchronize()
+            results[key] = outs
+        except Exception as exc:  # reported by the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=work, args=("a", A1)),
+               threading.Thread(target=work, args=("b", A2))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for key in ("a", "b"):
+        H0, t0 = ref[key]
+        assert len(results[key]) == 6
+        for H, tau in results[key]:
+            assert torch.equal(H, H0) and torch.equal(tau, t0)
+
+
 @pytest.mark.parametrize("lookahead", ["1", "0"])
 @pytest.mark.parametrize("n", [100, 700, 1100])
 def test_first_block_reads_padded_input_directly(monkeypatch, n, lookahead):
