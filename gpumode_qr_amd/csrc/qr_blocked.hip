@@ -433,6 +433,17 @@ hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r
 #define QR_PANEL_CASE(NWV, RLV)                                                             \
   hipLaunchKernelGGL((k_panel<NWV, RLV>), dim3(batch), dim3(64 * NWV), 0, stream, H, sHb, ldh, \
                      J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda)
+  // More matrices than CUs (a throughput-bound call): panels of up to 256 rows
+  // run 4 waves, so that more of them share a CU. Only for p < 4: panel p's
+  // diagonal tile is tile 0 of wave p. With few matrices the 8-wave panel's
+  // shorter per-wave work wins.
+  if (p < 4 && r <= 256 && batch > device_cu_count()) {
+    if (r <= 128)
+      QR_PANEL_CASE(4, 8);
+    else
+      QR_PANEL_CASE(4, 16);
+    return hipGetLastError();
+  }
   QR_STRIP_DISPATCH(r, QR_PANEL_CASE)
 #undef QR_PANEL_CASE
   return hipGetLastError();
