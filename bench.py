@@ -58,9 +58,9 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 # profile_run runs first (FETCH x2.000, WRITE x1.000). Counters cannot be read
 # from inside this process; rerun those commands after changing a kernel.
 HBM_MIB_PER_CALL = {
-    "smalln": {2: 32.9 + 32.7},
-    "panel": {3: 1547.0 + 381.3, 4: 459.9 + 140.2, 5: 495.5 + 134.1},
-    "trail": {3: 2487.1 + 1697.1, 4: 1803.7 + 1445.1, 5: 3254.4 + 2809.4},
+    "smalln": {2: 32.9 + 32.8},
+    "panel": {3: 1534.2 + 381.3, 4: 459.9 + 140.2, 5: 495.5 + 134.1},
+    "trail": {3: 2491.1 + 1697.2, 4: 1806.7 + 1443.8, 5: 3252.8 + 2806.5},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
