@@ -130,6 +130,41 @@ def test_panel_left_looking_vs_oracle(oracle, r, p, kw):
         assert np.abs(T[:kw, :kw] - Trefs[p]).max() <= 4 * tol, "T"
 
 
+@pytest.mark.parametrize("r,p,kw", [(100, 0, 16), (120, 3, 16), (200, 2, 16), (250, 3, 9)])
+def test_panel_many_matrices_vs_oracle(oracle, r, p, kw):
+    """More matrices than CUs: panels of up to 256 rows run the 4-wave kernel.
+    Three distinct blocks, each repeated 100 times, against the oracle."""
+    _say(f"panel batch 300 r={r} p={p} kw={kw}")
+    g = torch.Generator().manual_seed(r + 11 * p + kw)
+    blk = torch.randn(3, r, 16 * p + kw, generator=g).numpy()
+    starts, T_prev, refs = [], [], []
+    for b in range(3):
+        Hpre, _, Ts = _oracle_panels(oracle, blk[b][:, :16 * p], p) if p else (
+            np.zeros((r, 0), np.float32), None, [])
+        starts.append(np.concatenate([Hpre, blk[b][:, 16 * p:]], axis=1))
+        T_prev.append(np.stack(Ts) if p else None)
+        refs.append(_oracle_panels(oracle, blk[b], p + 1))
+    reps = 100
+    start = torch.from_numpy(np.repeat(np.stack(starts), reps, axis=0)).to(DEV)
+    Tp = torch.from_numpy(np.repeat(np.stack(T_prev), reps, axis=0)).to(DEV) if p else None
+    Hg, tau, T = hip_qr.panel(start, p=p, T_prev=Tp)
+    torch.cuda.synchronize()
+    Hg, tau, T = Hg.cpu().numpy(), tau.cpu().numpy(), T.cpu().numpy()
+    tol = 4 * r * 2**-23
+    up = np.triu(np.ones((r, kw), bool), k=-16 * p)
+    for i in range(3 * reps):
+        b = i // reps
+        Href, taus, Trefs = refs[b]
+        colnorm = np.linalg.norm(blk[b][:, 16 * p:].astype(np.float64), axis=0)
+        dH = np.abs(Hg[i][:, 16 * p:].astype(np.float64) - Href[:, 16 * p:])
+        assert (np.where(up, dH / colnorm, 0)).max() <= tol, ("R", i)
+        assert (np.where(~up, dH, 0)).max() <= tol, ("V", i)
+        assert np.abs(tau[i] - taus[p]).max() <= tol, ("tau", i)
+        assert np.abs(T[i][:kw, :kw] - Trefs[p]).max() <= 4 * tol, ("T", i)
+        if i % reps:  # identical inputs give identical bits
+            assert np.array_equal(Hg[i], Hg[i - 1]) and np.array_equal(tau[i], tau[i - 1])
+
+
 @pytest.mark.parametrize("m,k", [(16, 16), (64, 16), (300, 32), (1000, 64), (40, 7)])
 def test_larft_vs_oracle(oracle, m, k):
     _say(f"larft m={m} k={k}")
