@@ -252,7 +252,7 @@ def main() -> int:
 
     _lib.load()
     cfgs = [int(c) for c in args.configs.split(",") if c.strip()]
-    trace_kernels = ["smalln", "panel", "trail", "copy"]
+    trace_kernels = ["smalln", "panel", "trail", "copy", "cholqr"]
     rows = [run_config(c, args.steps, args.warmup, torch, trace_kernels, not args.no_orgqr)
             for c in cfgs]
     gm = bench.geomean([r["median_ms"] for r in rows])

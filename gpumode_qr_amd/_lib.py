@@ -67,7 +67,7 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 # qr_kernel_id values of include/qr_gfx950.h
-KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4, "apply": 5}
+KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4, "apply": 5, "cholqr": 6}
 
 ABI_VERSION = 3
 

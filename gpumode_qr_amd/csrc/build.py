@@ -21,7 +21,10 @@ OUT_DIR = PKG / "_build"
 LIB = PKG / "libqr_gfx950.so"
 ARCH = "gfx950"
 
-SOURCES = ["qr_smalln.hip", "qr_blocked.hip", "qr_apply.hip", "qr_larft.hip", "qr_copy.hip", "qr_api.hip"]
+SOURCES = [
+    "qr_smalln.hip", "qr_blocked.hip", "qr_cholqr.hip", "qr_apply.hip", "qr_larft.hip",
+    "qr_copy.hip", "qr_api.hip",
+]
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (the host
 # pass warns that it does not know the feature; that is expected).

@@ -24,7 +24,13 @@ hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t
                                float* tau, int batch, int n, hipStream_t stream);
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
                         float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
-                        int64_t sAb, int64_t lda, int batch, hipStream_t stream);
+                        int64_t sAb, int64_t lda, int batch, hipStream_t stream,
+                        const int* only);
+size_t cq_workspace_floats(int batch);
+hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
+                           int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
+                           int64_t sTwb, float* ws, int batch, hipStream_t stream);
+const int* cq_flags(float* ws, int batch);
 hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
                         int ncols, const float* Tws, int64_t sTwb, const float* A, int64_t sAb,
                         int64_t lda, int batch, hipStream_t stream);
@@ -58,6 +64,29 @@ size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 // Workspace of the blocked route: per matrix, the 16 x 16 T of each panel of
 // the current outer block.
 size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kTStride * sizeof(float)); }
+
+// Workspace of the CholeskyQR2 block route (Gram partials, 64 x 64 factors,
+// per-matrix fallback flags); reused by every block of a call.
+size_t ws_cq_bytes(int batch) { return align_up(qr::cq_workspace_floats(batch) * sizeof(float)); }
+
+// Outer blocks of 64 columns with at least this many rows take the CholeskyQR2
+// route: by default only in calls of at most kCqMaxBatch matrices, where the
+// Householder panels' column steps are the critical path. QR_CHOLQR=0
+// switches the route off, QR_CHOLQR=1 allows it at any batch size,
+// QR_CHOLQR_MIN_ROWS overrides the row bound (the route needs r > 64).
+constexpr int kCqMaxBatch = 16;
+int cq_min_rows(int batch) {
+  bool any_batch = false;
+  if (const char* env = std::getenv("QR_CHOLQR")) {
+    if (env[0] == '0') return 1 << 30;
+    any_batch = env[0] == '1';
+  }
+  if (const char* env = std::getenv("QR_CHOLQR_MIN_ROWS")) {
+    const int v = std::atoi(env);
+    if (v > 64) return v;
+  }
+  return (any_batch || batch <= kCqMaxBatch) ? 256 : 1 << 30;
+}
 
 
 // Panels per outer block for size n (QR_OUTER_BLOCKS=1..8 overrides).
@@ -171,13 +200,28 @@ hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, flo
 // (row stride lda, unit column stride); the results still go to H.
 hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw, float* tau,
                      int64_t sTaub, float* T, int64_t sTb, int batch, hipStream_t s,
-                     const float* A = nullptr, int64_t sAb = 0, int64_t lda = 0) {
+                     const float* A = nullptr, int64_t sAb = 0, int64_t lda = 0,
+                     const int* only = nullptr) {
   // left-looking MFMA work (panels 0..p-1) + the panel's own factorisation
   const double flops = (4.0 * r * kPanel * kPanel * p + panel_flops(r - 16 * p, kw)) * batch;
   const double bytes = (2.0 * r * kw + (double)r * kPanel * p + kw + kPanel * kPanel * (p + 1)) *
                        4.0 * batch;
   return traced(QR_KERNEL_PANEL, flops, bytes, s, [&] {
-    return qr::launch_panel(H, sHb, ldh, J0, p, r, kw, tau, sTaub, T, sTb, A, sAb, lda, batch, s);
+    return qr::launch_panel(H, sHb, ldh, J0, p, r, kw, tau, sTaub, T, sTb, A, sAb, lda, batch, s,
+                            only);
+  });
+}
+
+// One 64-column block by CholeskyQR2 + Householder reconstruction. Work per
+// matrix: four r x 64 x 64 MFMA passes at 5/8 density (two Grams, A M1, the
+// rows below times M); bytes: the block read three times, V written once.
+hipError_t run_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
+                        int64_t ldh, int r, float* tau, int64_t sTaub, float* T, int64_t sTb,
+                        float* ws, int batch, hipStream_t s) {
+  const double flops = 4.0 * 2.0 * r * 64.0 * 64.0 * 0.625 * batch;
+  const double bytes = 4.0 * r * 64.0 * 4.0 * batch;
+  return traced(QR_KERNEL_CHOLQR, flops, bytes, s, [&] {
+    return qr::launch_cq_block(Src, sSb, lds, Hb, sHb, ldh, r, tau, sTaub, T, sTb, ws, batch, s);
   });
 }
 
@@ -275,7 +319,7 @@ int qr_max_n(void) { return kMaxN; }
 
 size_t qr_geqrf_f32_workspace(int batch, int n) {
   if (batch <= 0 || n <= kSmallN || n > kMaxN) return 0;
-  return 2 * ws_t_bytes(batch);
+  return 2 * ws_t_bytes(batch) + ws_cq_bytes(batch);
 }
 
 int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
@@ -300,6 +344,8 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   // block k+1 never overwrite T factors that block k's trailing update reads.
   float* Tslot[2] = {static_cast<float*>(workspace),
                      static_cast<float*>(workspace) + (size_t)batch * kTStride};
+  float* cq_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * ws_t_bytes(batch));
+  const int cq_rows = cq_min_rows(batch);
 
   // With a unit column stride the first outer block reads A itself: its panels
   // and trailing updates write every element of H, so no copy is needed.
@@ -335,9 +381,20 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
     const float* Ab = (direct && J0 == 0) ? A : nullptr;  // source of this block's columns
     const int r = n - J0;
     const int nblk = (r + kPanel - 1) / kPanel < P ? (r + kPanel - 1) / kPanel : P;
+    // A full 64-column block with enough rows: CholeskyQR2 + reconstruction,
+    // then the panels for the matrices it flagged (the rest return at once).
+    const int* only = nullptr;
+    if (P * kPanel == 64 && J0 + 64 <= n && r >= cq_rows) {
+      const float* Src = Ab ? Ab : H + (int64_t)J0 * n + J0;
+      const int64_t sSb = Ab ? sAb : nn, lds = Ab ? sAr : n;
+      e = run_cq_block(Src, sSb, lds, H + (int64_t)J0 * n + J0, nn, n, r, tau + J0, n, Tws,
+                       kTStride, cq_ws, batch, s);
+      if (e != hipSuccess) return QR_ELAUNCH;
+      only = qr::cq_flags(cq_ws, batch);
+    }
     for (int p = 0; p < nblk; ++p) {
       const int kw = (r - kPanel * p) < kPanel ? (r - kPanel * p) : kPanel;
-      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s, Ab, sAb, sAr);
+      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s, Ab, sAb, sAr, only);
       if (e != hipSuccess) return QR_ELAUNCH;
     }
     const int ncols = r - kPanel * nblk;

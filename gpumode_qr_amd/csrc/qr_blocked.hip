@@ -288,17 +288,21 @@ constexpr bool kPanelFastPass = QR_PANEL_FAST != 0;
 // Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
 // Writes V_p / R in place, tau_p, and T_p at Tb + 256 p. The panel's columns are
 // read from H, or from A (row stride lda, unit column stride) when A is not
-// null: the first outer block reads the caller's matrix directly.
+// null: the first outer block reads the caller's matrix directly. When `only`
+// is not null, only matrices b with only[b] != 0 are factored (the others
+// return at once).
 template <int NW, int RL>
 __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
                                                    int64_t ldh, int J0, int p, int r, int kw,
                                                    float* __restrict__ tau, int64_t sTaub,
                                                    float* __restrict__ Tws, int64_t sTwb,
-                                                   const float* A, int64_t sAb, int64_t lda) {
+                                                   const float* A, int64_t sAb, int64_t lda,
+                                                   const int* __restrict__ only) {
   using S = Strip<NW, RL>;
   __shared__ PanelShared<NW, RL> sh;
 
   const int b = blockIdx.x;
+  if (only && only[b] == 0) return;  // this matrix's block was factored elsewhere
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int k = lane & 15, g = lane >> 4;
@@ -427,12 +431,13 @@ __global__ __launch_bounds__(64 * NW) void k_trail(float* __restrict__ H, int64_
 
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
                         float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
-                        int64_t sAb, int64_t lda, int batch, hipStream_t stream) {
+                        int64_t sAb, int64_t lda, int batch, hipStream_t stream,
+                        const int* only) {
   if (kw < 1 || kw > 16 || p < 0 || p >= kMaxBlocks || r > kMaxStripRows || r < 16 * p + kw)
     return hipErrorInvalidValue;
 #define QR_PANEL_CASE(NWV, RLV)                                                             \
   hipLaunchKernelGGL((k_panel<NWV, RLV>), dim3(batch), dim3(64 * NWV), 0, stream, H, sHb, ldh, \
-                     J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda)
+                     J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda, only)
   // More matrices than CUs (a throughput-bound call): panels of up to 256 rows
   // run 4 waves, so that more of them share a CU. Only for p < 4: panel p's
   // diagonal tile is tile 0 of wave p. With few matrices the 8-wave panel's

@@ -38,7 +38,8 @@ typedef enum qr_kernel_id {
   QR_KERNEL_TRAIL = 2,  /* kernel (d), trailing compact-WY update */
   QR_KERNEL_COPY = 3,   /* A -> H copy (only for A without a unit column stride) */
   QR_KERNEL_LARFT = 4,  /* kernel (c) */
-  QR_KERNEL_APPLY = 5   /* block-reflector application of orgqr / ormqr */
+  QR_KERNEL_APPLY = 5,  /* block-reflector application of orgqr / ormqr */
+  QR_KERNEL_CHOLQR = 6  /* CholeskyQR2 + reconstruction of a 64-column block (its 4-5 launches) */
 } qr_kernel_id;
 
 /* Human-readable text for a qr_status value (static storage). */

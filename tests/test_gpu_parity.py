@@ -574,3 +574,112 @@ def test_run_baseline_db_record_schema(tmp_path):
     assert ps["cpu_geqrf_ms"] > 0 and extra["cpu_cores"] >= 1
     assert ps["counters"]["smalln"]["launches_per_call"] == 1.0
     assert set(ps["counters"]) == {"smalln"}  # n = 32 runs the one fused launch
+
+
+# --------------------------------------------------------------------------
+# Outer blocks by CholeskyQR2 + Householder reconstruction (qr_cholqr.hip).
+# QR_CHOLQR_MIN_ROWS=64 sends every full 64-column block through the route
+# (by default only blocks of >= 256 rows take it); QR_CHOLQR=0 switches it off.
+
+@pytest.mark.parametrize("n", [128, 129, 200, 256, 300, 513, 1100])
+def test_cholqr_route_vs_oracle(monkeypatch, oracle, n):
+    _say(f"cholqr route (every full block) n={n}")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
+    A = _gauss(3, n, seed=n + 11)
+    H, tau = _run(A)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"cholqr n={n}")
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+
+
+def test_cholqr_route_cond1e2_svd(monkeypatch, oracle):
+    _say("cholqr route, cond-1e2 SVD input b2 n512")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
+    A = inputs.svd_matrices(2, 512, 2.0, torch.Generator().manual_seed(5))
+    A = A.float()
+    H, tau = _run(A)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="cholqr svd")
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+
+
+# A block whose Gram is singular, out of range, or too ill-conditioned for
+# CholeskyQR2 falls back to the Householder panels for that matrix only; the
+# other matrices of the batch keep the route in the same block.
+@pytest.mark.parametrize("n,cols", [(300, (20, 150, 290)), (700, (5, 400, 650))])
+@pytest.mark.parametrize("kind", ["zero", "tiny", "huge", "denormal", "near_dup"])
+def test_cholqr_fallback_vs_oracle(monkeypatch, oracle, n, cols, kind):
+    _say(f"cholqr fallback {kind} n={n} cols={cols}")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
+    A = _gauss(3, n, seed=n + 3)
+    for b, c in ((0, cols[0]), (1, cols[1]), (1, cols[2])):
+        if kind == "zero":
+            A[b, :, c] = 0.0
+        elif kind == "near_dup":  # columns c and c+1 agree to 1e-6: scaled pivot ~1e-12
+            A[b, :, c + 1 if c + 1 < n else c - 1] = A[b, :, c] * (1 + 1e-6)
+        else:
+            A[b, :, c] *= {"tiny": 1e-30, "huge": 1e25, "denormal": 1e-40}[kind]
+    H, tau = _run(A)
+    assert torch.isfinite(H).all() and torch.isfinite(tau).all()
+    if kind != "near_dup":  # near-duplicate columns: kappa ~1e7, gates only
+        H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+        assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref,
+                      what=f"cholqr fallback {kind}")
+    if kind in ("zero", "near_dup"):
+        res = checker.check(A, H, tau)
+        assert res.passed, res.as_dict()
+
+
+@pytest.mark.parametrize("n,batch", [(300, 3), (1100, 2), (700, 64)])
+def test_cholqr_lookahead_and_repeat_bitwise(monkeypatch, n, batch):
+    _say(f"cholqr route look-ahead on/off and repeat n={n} b={batch}")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
+    A = _gauss(batch, n, seed=n + 5).to(DEV)
+    monkeypatch.setenv("QR_LOOKAHEAD", "0")
+    H0, t0 = hip_qr.geqrf(A)
+    torch.cuda.synchronize()
+    monkeypatch.setenv("QR_LOOKAHEAD", "1")
+    H1, t1 = hip_qr.geqrf(A)
+    H2, t2 = hip_qr.geqrf(A)
+    torch.cuda.synchronize()
+    assert torch.equal(H0, H1) and torch.equal(t0, t1)
+    assert torch.equal(H1, H2) and torch.equal(t1, t2)
+
+
+def test_cholqr_off_matches_on_within_tolerance(monkeypatch, oracle):
+    _say("cholqr on vs off, b4 n600")
+    A = _gauss(4, 600, seed=77)
+    monkeypatch.setenv("QR_CHOLQR", "0")
+    Hh, th = _run(A)
+    monkeypatch.delenv("QR_CHOLQR")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
+    Hc, tc = _run(A)
+    assert not torch.equal(Hh, Hc)  # the two routes round differently
+    assert_parity(A.numpy(), Hc.numpy(), tc.numpy(), Hh.numpy().astype(np.float64),
+                  th.numpy().astype(np.float64), what="cholqr vs householder")
+
+
+@pytest.mark.parametrize("kind", ["upper", "block_diag"])
+def test_cholqr_exact_zero_structure(monkeypatch, oracle, kind):
+    """Exact zeros below a diagonal give slarfg's tau = 0: upper-triangular input
+    stays a fixed point (H == A, tau == 0) and a block-diagonal matrix matches
+    the oracle, because such blocks leave the CholeskyQR2 route."""
+    _say(f"cholqr route, exact-zero structure {kind} n=300")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "65")
+    A = _gauss(2, 300, seed=9)
+    if kind == "upper":
+        A = torch.triu(A)
+        A.diagonal(dim1=1, dim2=2).abs_().add_(1.0)
+    else:
+        mask = torch.zeros(300, 300, dtype=torch.bool)
+        for s0 in range(0, 300, 100):
+            mask[s0:s0 + 100, s0:s0 + 100] = True
+        A = torch.where(mask, A, torch.zeros(()))
+    H, tau = _run(A)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"cholqr {kind}")
+    if kind == "upper":
+        assert torch.equal(tau, torch.zeros_like(tau))
+        assert torch.equal(H, A)
