@@ -26,11 +26,16 @@ hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r
                         float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
                         int64_t sAb, int64_t lda, int batch, hipStream_t stream,
                         const int* only);
+hipError_t launch_panel_seq(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r,
+                            float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
+                            int64_t sAb, int64_t lda, int batch, hipStream_t stream,
+                            const int* only);
 size_t cq_workspace_floats(int batch);
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
                            int64_t sTwb, float* ws, int batch, hipStream_t stream);
 const int* cq_flags(float* ws, int batch);
+hipError_t launch_cq_reset(float* ws, int batch, hipStream_t stream);
 hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
                         int ncols, const float* Tws, int64_t sTwb, const float* A, int64_t sAb,
                         int64_t lda, int batch, hipStream_t stream);
@@ -83,9 +88,9 @@ int cq_min_rows(int batch) {
   }
   if (const char* env = std::getenv("QR_CHOLQR_MIN_ROWS")) {
     const int v = std::atoi(env);
-    if (v > 64) return v;
+    if (v >= 64) return v > 64 ? v : 65;
   }
-  return (any_batch || batch <= kCqMaxBatch) ? 256 : 1 << 30;
+  return (any_batch || batch <= kCqMaxBatch) ? 512 : 1 << 30;
 }
 
 
@@ -346,6 +351,7 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
                      static_cast<float*>(workspace) + (size_t)batch * kTStride};
   float* cq_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * ws_t_bytes(batch));
   const int cq_rows = cq_min_rows(batch);
+  bool cq_ready = false;
 
   // With a unit column stride the first outer block reads A itself: its panels
   // and trailing updates write every element of H, so no copy is needed.
@@ -385,6 +391,10 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
     // then the panels for the matrices it flagged (the rest return at once).
     const int* only = nullptr;
     if (P * kPanel == 64 && J0 + 64 <= n && r >= cq_rows) {
+      if (!cq_ready) {  // arrival counters of the fused Gram kernels start at zero
+        if (qr::launch_cq_reset(cq_ws, batch, s) != hipSuccess) return QR_ELAUNCH;
+        cq_ready = true;
+      }
       const float* Src = Ab ? Ab : H + (int64_t)J0 * n + J0;
       const int64_t sSb = Ab ? sAb : nn, lds = Ab ? sAr : n;
       e = run_cq_block(Src, sSb, lds, H + (int64_t)J0 * n + J0, nn, n, r, tau + J0, n, Tws,
@@ -392,9 +402,16 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
       if (e != hipSuccess) return QR_ELAUNCH;
       only = qr::cq_flags(cq_ws, batch);
     }
-    for (int p = 0; p < nblk; ++p) {
+    if (only) {  // one launch for the flagged matrices' panels
+      e = traced(QR_KERNEL_PANEL, 0.0, 0.0, s, [&] {
+        return qr::launch_panel_seq(H, nn, n, J0, nblk, r, tau, n, Tws, kTStride, Ab, sAb, sAr,
+                                    batch, s, only);
+      });
+      if (e != hipSuccess) return QR_ELAUNCH;
+    }
+    for (int p = 0; p < nblk && !only; ++p) {
       const int kw = (r - kPanel * p) < kPanel ? (r - kPanel * p) : kPanel;
-      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s, Ab, sAb, sAr, only);
+      e = run_panel(H, nn, n, J0, p, r, kw, tau, n, Tws, kTStride, batch, s, Ab, sAb, sAr);
       if (e != hipSuccess) return QR_ELAUNCH;
     }
     const int ncols = r - kPanel * nblk;

@@ -284,25 +284,14 @@ __device__ __forceinline__ void panel_load_apply(float (&c)[1][RL], const float*
 #endif
 constexpr bool kPanelFastPass = QR_PANEL_FAST != 0;
 
-// Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
-// Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
-// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p. The panel's columns are
-// read from H, or from A (row stride lda, unit column stride) when A is not
-// null: the first outer block reads the caller's matrix directly. When `only`
-// is not null, only matrices b with only[b] != 0 are factored (the others
-// return at once).
+// Body of the panel kernels: factor panel p of matrix b (see k_panel).
 template <int NW, int RL>
-__global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
-                                                   int64_t ldh, int J0, int p, int r, int kw,
-                                                   float* __restrict__ tau, int64_t sTaub,
-                                                   float* __restrict__ Tws, int64_t sTwb,
-                                                   const float* A, int64_t sAb, int64_t lda,
-                                                   const int* __restrict__ only) {
+__device__ __forceinline__ void panel_factor(PanelShared<NW, RL>& sh, int b, float* __restrict__ H,
+                                             int64_t sHb, int64_t ldh, int J0, int p, int r,
+                                             int kw, float* __restrict__ tau, int64_t sTaub,
+                                             float* __restrict__ Tws, int64_t sTwb,
+                                             const float* A, int64_t sAb, int64_t lda) {
   using S = Strip<NW, RL>;
-  __shared__ PanelShared<NW, RL> sh;
-
-  const int b = blockIdx.x;
-  if (only && only[b] == 0) return;  // this matrix's block was factored elsewhere
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int k = lane & 15, g = lane >> 4;
@@ -347,7 +336,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
   // T_p (16 x 16, upper): T[j][j] = tau_j, T[0:j, j] = -tau_j T[0:j, 0:j] z_j.
   // Lane k of wave 0 holds row k of T in registers; z_j rows are b128 reads.
   // Only wave 0 wrote zbuf and writes taus, so a wave-level sync suffices.
-  if (w != 0) return;
+  if (w != 0) return;  // the caller synchronises the workgroup before reusing sh
   if (g == 0) sh.taus[k] = (k < kw) ? st.tau : 0.0f;
   wave_sync();
   if (g == 0) {
@@ -378,6 +367,47 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
 #pragma unroll
     for (int q = 0; q < 16; ++q) Tp[k * 16 + q] = trow[q];
     if (k < kw) tau[(int64_t)b * sTaub + J0 + d0 + k] = st.tau;
+  }
+}
+
+// Factor panel p (columns 16p..16p+kw-1 of the outer block whose top-left is
+// Blk, r rows) after applying panels 0..p-1 of the block (their T's at Tb).
+// Writes V_p / R in place, tau_p, and T_p at Tb + 256 p. The panel's columns are
+// read from H, or from A (row stride lda, unit column stride) when A is not
+// null: the first outer block reads the caller's matrix directly. When `only`
+// is not null, only matrices b with only[b] != 0 are factored (the others
+// return at once).
+template <int NW, int RL>
+__global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
+                                                   int64_t ldh, int J0, int p, int r, int kw,
+                                                   float* __restrict__ tau, int64_t sTaub,
+                                                   float* __restrict__ Tws, int64_t sTwb,
+                                                   const float* A, int64_t sAb, int64_t lda,
+                                                   const int* __restrict__ only) {
+  __shared__ PanelShared<NW, RL> sh;
+  const int b = blockIdx.x;
+  if (only && only[b] == 0) return;  // this matrix's block was factored elsewhere
+  panel_factor<NW, RL>(sh, b, H, sHb, ldh, J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda);
+}
+
+// Panels 0..nblk-1 of the outer block, one after the other in one workgroup
+// per matrix, for the matrices b with only[b] != 0 (the others return at
+// once). Panel p + 1 reads V_p, T_p from global memory after the workgroup
+// barrier that ends panel p.
+template <int NW, int RL>
+__global__ __launch_bounds__(64 * NW) void k_panel_seq(float* __restrict__ H, int64_t sHb,
+                                                       int64_t ldh, int J0, int nblk, int r,
+                                                       float* __restrict__ tau, int64_t sTaub,
+                                                       float* __restrict__ Tws, int64_t sTwb,
+                                                       const float* A, int64_t sAb, int64_t lda,
+                                                       const int* __restrict__ only) {
+  __shared__ PanelShared<NW, RL> sh;
+  const int b = blockIdx.x;
+  if (only[b] == 0) return;
+  for (int p = 0; p < nblk; ++p) {
+    const int kw = (r - 16 * p) < 16 ? (r - 16 * p) : 16;
+    panel_factor<NW, RL>(sh, b, H, sHb, ldh, J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda);
+    __syncthreads();
   }
 }
 
@@ -451,6 +481,20 @@ hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r
   }
   QR_STRIP_DISPATCH(r, QR_PANEL_CASE)
 #undef QR_PANEL_CASE
+  return hipGetLastError();
+}
+
+hipError_t launch_panel_seq(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r,
+                            float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
+                            int64_t sAb, int64_t lda, int batch, hipStream_t stream,
+                            const int* only) {
+  if (!only || nblk < 1 || nblk > kMaxBlocks || r > kMaxStripRows || r < 16 * (nblk - 1) + 1)
+    return hipErrorInvalidValue;
+#define QR_PANEL_SEQ_CASE(NWV, RLV)                                                            \
+  hipLaunchKernelGGL((k_panel_seq<NWV, RLV>), dim3(batch), dim3(64 * NWV), 0, stream, H, sHb, \
+                     ldh, J0, nblk, r, tau, sTaub, Tws, sTwb, A, sAb, lda, only)
+  QR_STRIP_DISPATCH(r, QR_PANEL_SEQ_CASE)
+#undef QR_PANEL_SEQ_CASE
   return hipGetLastError();
 }
 

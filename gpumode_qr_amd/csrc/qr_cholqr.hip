@@ -30,6 +30,8 @@
 // A matrix that fails any of them gets its flag set and none of its outputs
 // written; the panel launches that follow factor exactly those matrices by
 // Householder column steps and return at once for the others.
+#include <cstdlib>
+
 #include "qr_wy.hpp"
 
 namespace qr {
@@ -90,90 +92,6 @@ __device__ __forceinline__ void cq_tile_times_m(f32x4 (&x)[4], const float* __re
     for (int J = 0; J < 4; ++J)
       if (s <= 4 * J + 3)
         x[J] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], mr[2 * J * (J + 1) + s], x[J], 0, 0, 0);
-}
-
-// ---------------------------------------------------------------------------
-// Gram partials: workgroup (b, c) sums X^T X over rows [c rc, (c+1) rc) of the
-// block (X = A_b, or A_b M1 in pass 2) and writes the 10 upper 16 x 16 tiles,
-// each row-major, to part[(b nchunk + c) kCqSlot]. Pass 1 also writes, after
-// the tiles, the mask of columns with a nonzero entry in rows >= 64 of the
-// chunk. Four waves, rc / 4 rows each.
-template <bool kPass2>
-__global__ __launch_bounds__(256) void k_cq_gram(const float* __restrict__ Src, int64_t sSb,
-                                                 int64_t lds, int r, int rc, int nchunk,
-                                                 const float* __restrict__ M1, int64_t sMb,
-                                                 float* __restrict__ part,
-                                                 const int* __restrict__ flags) {
-  __shared__ float red[4][kCqPart];
-  const int b = blockIdx.x / nchunk;
-  const int c = blockIdx.x - b * nchunk;
-  if (kPass2 && flags[b] != 0) return;
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int k = lane & 15, g = lane >> 4;
-  const float* S = Src + (int64_t)b * sSb;
-
-  f32x4 acc[kCqTiles];
-#pragma unroll
-  for (int t = 0; t < kCqTiles; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float mr[40];
-  if constexpr (kPass2) cq_load_mb(mr, M1 + (int64_t)b * sMb, lane);
-
-  const int rw = rc >> 2;
-  const int rbeg = c * rc + w * rw;
-  bool nz[4] = {false, false, false, false};  // pass 1: column 16I + k nonzero below row 64
-  for (int t = 0; t < rw; t += 16) {
-    const int row0 = rbeg + t;
-    if (row0 >= r) break;
-    f32x4 x[4];
-    if constexpr (kPass2) {
-      cq_tile_times_m(x, S, lds, row0, r, mr, lane);
-    } else {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = row0 + 4 * g + v;
-        const float* p = S + (int64_t)row * lds + k;
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          x[I][v] = (row < r) ? p[16 * I] : 0.0f;
-          nz[I] = nz[I] || (row >= kCqB && x[I][v] != 0.0f);
-        }
-      }
-    }
-    // G_IJ += X_I^T X_J: the accumulator layout with K order {v, v+4, v+8,
-    // v+12} is the A and the B operand layout at once.
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int J = I; J < 4; ++J)
-          acc[cq_tile(I, J)] =
-              __builtin_amdgcn_mfma_f32_16x16x4f32(x[I][v], x[J][v], acc[cq_tile(I, J)], 0, 0, 0);
-  }
-#pragma unroll
-  for (int t = 0; t < kCqTiles; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[w][t * 256 + (4 * g + v) * 16 + k] = acc[t][v];
-  __shared__ unsigned long long wmask[4];
-  if constexpr (!kPass2) {
-    // Lane 16 g' + k of the ballot for tile I: column 16 I + k, rows 4 g' + v.
-    unsigned long long m = 0;
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      unsigned long long bl = __ballot(nz[I]);
-      bl |= bl >> 32;
-      bl |= bl >> 16;
-      m |= (bl & 0xFFFFull) << (16 * I);
-    }
-    if (lane == 0) wmask[w] = m;
-  }
-  __syncthreads();
-  float* dst = part + (int64_t)blockIdx.x * kCqSlot;
-  for (int e = threadIdx.x; e < kCqPart; e += 256)
-    dst[e] = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
-  if (!kPass2 && threadIdx.x == 0)
-    *reinterpret_cast<unsigned long long*>(dst + kCqPart) = wmask[0] | wmask[1] | wmask[2] | wmask[3];
 }
 
 // The 64 x 64 Gram of matrix b from its nchunk partials into G (row stride
@@ -514,20 +432,21 @@ __device__ __forceinline__ void cq_store_rows(float* __restrict__ Z, int64_t ldz
 // ---------------------------------------------------------------------------
 // Pass 1 per matrix: scaled Cholesky of G1, guard, M1 = R1^-1 and R1 into the
 // workspace (mats[b]: M1 at 0, R1 at kCqMat), flag[b] = 0 (ok) or 1.
-__global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part, int nchunk,
-                                                  float* __restrict__ mats, int64_t sMb,
-                                                  int* __restrict__ flags) {
-  __shared__ float G[kCqB * kCqLS];
-  __shared__ float Ri[kCqB * kCqLS];
-  __shared__ float piv[64];
-  __shared__ float dsc[64];   // d_j = sqrt(G1_jj)
-  __shared__ float rdsc[64];  // 1 / d_j
-  __shared__ int dbad;
-  const int b = blockIdx.x;
+constexpr int kCqChol1Lds = 2 * kCqB * kCqLS + 4 * 64;  // floats
+__device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
+                                              const float* __restrict__ part, int nchunk,
+                                              float* __restrict__ mats, int64_t sMb,
+                                              int* __restrict__ flags) {
+  float* const G = smem;
+  float* const Ri = G + kCqB * kCqLS;
+  float* const piv = Ri + kCqB * kCqLS;
+  float* const dsc = piv + 64;   // d_j = sqrt(G1_jj)
+  float* const rdsc = dsc + 64;  // 1 / d_j
+  int* const dbad = reinterpret_cast<int*>(rdsc + 64);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   cq_sum_gram(G, part, b, nchunk);
-  if (threadIdx.x == 0) dbad = 0;
+  if (threadIdx.x == 0) *dbad = 0;
   __syncthreads();
   if (threadIdx.x < 64) {
     const int j = threadIdx.x;
@@ -536,7 +455,7 @@ __global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part
     const float dj = __builtin_amdgcn_sqrtf(dok ? gjj : 1.0f);
     dsc[j] = dj;
     rdsc[j] = __builtin_amdgcn_rcpf(dj);
-    if (!dok) dbad = 1;
+    if (!dok) *dbad = 1;
   }
   __syncthreads();
   for (int e = threadIdx.x; e < kCqMat; e += 256) {  // D^-1 G1 D^-1
@@ -559,7 +478,7 @@ __global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part
     for (int c = 0; c < nchunk; ++c)
       nzm |= *reinterpret_cast<const unsigned long long*>(
           part + ((int64_t)b * nchunk + c) * kCqSlot + kCqPart);
-    const bool ok = __all(piv[j] >= kCqPivMin && piv[j] <= 3.0e38f) && dbad == 0 &&
+    const bool ok = __all(piv[j] >= kCqPivMin && piv[j] <= 3.0e38f) && *dbad == 0 &&
                     nzm == ~0ull;
     if (j == 0) flags[b] = ok ? 0 : 1;
   }
@@ -571,32 +490,33 @@ __global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part
 // below, k_cq_form), T_qq, tau and the block's top 64 rows of H (R = S R_c on
 // and above the diagonal, L1 below). Nothing is written for a matrix whose
 // flag is or becomes set.
-__global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part, int nchunk,
-                                                  float* __restrict__ mats, int64_t sMb,
-                                                  int* __restrict__ flags,
-                                                  const float* __restrict__ Src, int64_t sSb,
-                                                  int64_t lds, float* __restrict__ Hb,
-                                                  int64_t sHb, int64_t ldh,
-                                                  float* __restrict__ tau, int64_t sTaub,
-                                                  float* __restrict__ Tws, int64_t sTwb) {
-  __shared__ float B[7][kCqB * kCqLS];  // 119 KB (+ 17 KB Li)
-  __shared__ float Li[kCqB * kCqLS];  // L_KK^-1 at rows 16K.., columns 0..15
-  __shared__ float piv[64];
-  __shared__ float sgn[64];
-  __shared__ float pinv[64];
-  __shared__ float devw[4];
-  __shared__ int okflag;
-  const int b = blockIdx.x;
-  if (flags[b] != 0) return;
+constexpr int kCqReconLds = 8 * kCqB * kCqLS + 4 * 64 + 8;  // floats (139 KB)
+__device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
+                                              const float* __restrict__ part, int nchunk,
+                                              float* __restrict__ mats, int64_t sMb,
+                                              int* __restrict__ flags,
+                                              const float* __restrict__ Src, int64_t sSb,
+                                              int64_t lds, float* __restrict__ Hb, int64_t sHb,
+                                              int64_t ldh, float* __restrict__ tau,
+                                              int64_t sTaub, float* __restrict__ Tws,
+                                              int64_t sTwb) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  float* const G2 = B[0];    // G2, then R2
-  float* const M1l = B[1];   // M1
-  float* const R1l = B[2];   // R1
-  float* const At = B[3];    // A_b[0:64], then Q_top, then L\U
-  float* const R2i = B[4];   // R2^-1, then U^-1
-  float* const Rinv = B[5];  // M1 R2^-1
-  float* const Rc = B[6];    // R2 R1
+  constexpr int kM = kCqB * kCqLS;
+  float* const G2 = smem;         // G2, then R2
+  float* const M1l = smem + kM;   // M1
+  float* const R1l = smem + 2 * kM;  // R1
+  float* const At = smem + 3 * kM;   // A_b[0:64], then Q_top, then L\U
+  float* const R2i = smem + 4 * kM;  // R2^-1, then U^-1
+  float* const Rinv = smem + 5 * kM;  // M1 R2^-1
+  float* const Rc = smem + 6 * kM;    // R2 R1
+  float* const Li = smem + 7 * kM;    // L_KK^-1 at rows 16K.., columns 0..15
+  float* const piv = smem + 8 * kM;
+  float* const sgn = piv + 64;
+  float* const pinv = sgn + 64;
+  float* const devw = pinv + 64;
+  int* const okflagp = reinterpret_cast<int*>(devw + 4);
+  int& okflag = *okflagp;
   const float* M1g = mats + (int64_t)b * sMb;
   const float* S = Src + (int64_t)b * sSb;
 
@@ -694,6 +614,139 @@ __global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part
 }
 
 // ---------------------------------------------------------------------------
+// Gram partials, fused with the per-matrix step. Workgroup (b, c) sums X^T X
+// over rows [c rc, (c+1) rc) of the block (X = A_b in pass 1, A_b M1 in pass
+// 2) and writes the 10 upper 16 x 16 tiles, each row-major, to
+// part[(b nchunk + c) kCqSlot]; pass 1 also writes, after the tiles, the mask
+// of columns with a nonzero entry in rows >= 64 of the chunk. The last of
+// matrix b's nchunk workgroups to finish (counted in cnt[b], which it resets
+// to zero) then runs the per-matrix step: cq_chol1_body in pass 1,
+// cq_recon_body in pass 2. Partials are summed in chunk order, so the result
+// does not depend on which workgroup is last. Four waves, rc / 4 rows each.
+template <bool kPass2, bool kFused>
+__global__ __launch_bounds__(256) void k_cq_gram(const float* __restrict__ Src, int64_t sSb,
+                                                 int64_t lds, int r, int rc, int nchunk,
+                                                 float* __restrict__ mats, int64_t sMb,
+                                                 float* __restrict__ part,
+                                                 int* __restrict__ flags, int* __restrict__ cnt,
+                                                 float* __restrict__ Hb, int64_t sHb, int64_t ldh,
+                                                 float* __restrict__ tau, int64_t sTaub,
+                                                 float* __restrict__ Tws, int64_t sTwb) {
+  constexpr int kRed = 4 * kCqPart + 8;
+  constexpr int kLds = !kFused ? kRed
+                               : (kPass2 ? kCqReconLds : (kCqChol1Lds > kRed ? kCqChol1Lds : kRed));
+  __shared__ __attribute__((aligned(16))) float smem[kLds];
+  float (*red)[kCqPart] = reinterpret_cast<float (*)[kCqPart]>(smem);
+  unsigned long long* wmask = reinterpret_cast<unsigned long long*>(smem + 4 * kCqPart);
+  __shared__ int last;
+  const int b = blockIdx.x / nchunk;
+  const int c = blockIdx.x - b * nchunk;
+  if (kPass2 && flags[b] != 0) return;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int k = lane & 15, g = lane >> 4;
+  const float* S = Src + (int64_t)b * sSb;
+
+  f32x4 acc[kCqTiles];
+#pragma unroll
+  for (int t = 0; t < kCqTiles; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mr[40];
+  if constexpr (kPass2) cq_load_mb(mr, mats + (int64_t)b * sMb, lane);
+
+  const int rw = rc >> 2;
+  const int rbeg = c * rc + w * rw;
+  bool nz[4] = {false, false, false, false};  // pass 1: column 16I + k nonzero below row 64
+  for (int t = 0; t < rw; t += 16) {
+    const int row0 = rbeg + t;
+    if (row0 >= r) break;
+    f32x4 x[4];
+    if constexpr (kPass2) {
+      cq_tile_times_m(x, S, lds, row0, r, mr, lane);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = row0 + 4 * g + v;
+        const float* p = S + (int64_t)row * lds + k;
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          x[I][v] = (row < r) ? p[16 * I] : 0.0f;
+          nz[I] = nz[I] || (row >= kCqB && x[I][v] != 0.0f);
+        }
+      }
+    }
+    // G_IJ += X_I^T X_J: the accumulator layout with K order {v, v+4, v+8,
+    // v+12} is the A and the B operand layout at once.
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int J = I; J < 4; ++J)
+          acc[cq_tile(I, J)] =
+              __builtin_amdgcn_mfma_f32_16x16x4f32(x[I][v], x[J][v], acc[cq_tile(I, J)], 0, 0, 0);
+  }
+#pragma unroll
+  for (int t = 0; t < kCqTiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[w][t * 256 + (4 * g + v) * 16 + k] = acc[t][v];
+  if constexpr (!kPass2) {
+    // Lane 16 g' + k of the ballot for tile I: column 16 I + k, rows 4 g' + v.
+    unsigned long long m = 0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      unsigned long long bl = __ballot(nz[I]);
+      bl |= bl >> 32;
+      bl |= bl >> 16;
+      m |= (bl & 0xFFFFull) << (16 * I);
+    }
+    if (lane == 0) wmask[w] = m;
+  }
+  __syncthreads();
+  float* dst = part + (int64_t)blockIdx.x * kCqSlot;
+  for (int e = threadIdx.x; e < kCqPart; e += 256)
+    dst[e] = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+  if (!kPass2 && threadIdx.x == 0)
+    *reinterpret_cast<unsigned long long*>(dst + kCqPart) = wmask[0] | wmask[1] | wmask[2] | wmask[3];
+  if constexpr (!kFused) return;
+  // Publish the partial, count it; the last workgroup of matrix b goes on.
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last = (atomicAdd(&cnt[b], 1) == nchunk - 1) ? 1 : 0;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (threadIdx.x == 0) cnt[b] = 0;
+  if constexpr (kPass2)
+    cq_recon_body(smem, b, part, nchunk, mats, sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau,
+                  sTaub, Tws, sTwb);
+  else
+    cq_chol1_body(smem, b, part, nchunk, mats, sMb, flags);
+}
+
+// The per-matrix steps as kernels of their own (one workgroup per matrix),
+// after Gram kernels launched without kFused.
+__global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part, int nchunk,
+                                                  float* __restrict__ mats, int64_t sMb,
+                                                  int* __restrict__ flags) {
+  __shared__ __attribute__((aligned(16))) float smem[kCqChol1Lds + 8];
+  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags);
+}
+
+__global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part, int nchunk,
+                                                  float* __restrict__ mats, int64_t sMb,
+                                                  int* __restrict__ flags,
+                                                  const float* __restrict__ Src, int64_t sSb,
+                                                  int64_t lds, float* __restrict__ Hb,
+                                                  int64_t sHb, int64_t ldh,
+                                                  float* __restrict__ tau, int64_t sTaub,
+                                                  float* __restrict__ Tws, int64_t sTwb) {
+  __shared__ __attribute__((aligned(16))) float smem[kCqReconLds];
+  if (flags[blockIdx.x] != 0) return;
+  cq_recon_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, Src, sSb, lds, Hb, sHb, ldh,
+                tau, sTaub, Tws, sTwb);
+}
+
+// ---------------------------------------------------------------------------
 // V below the top block: H rows 64 + [c rc, (c+1) rc) of the block = A_b M.
 __global__ __launch_bounds__(256) void k_cq_form(const float* __restrict__ Src, int64_t sSb,
                                                  int64_t lds, float* __restrict__ Hb,
@@ -743,15 +796,29 @@ void cq_chunks(int rows, int batch, int max_chunks, int* rc, int* nchunk) {
 
 constexpr int kCqMaxChunks = 16;
 
+// Fused Gram + per-matrix kernels (the last workgroup of a matrix finishes it)
+// save two launches per block but measured slower at every shape tried (b2
+// n4096 9.48 vs 9.19 ms, b16 n2048 7.07 vs 5.69 ms): the fused pass-2 kernel's
+// 137 KB of LDS per workgroup keeps its workgroups off the CUs that the
+// concurrent trailing update holds. Off by default; QR_CHOLQR_FUSED=1 selects
+// them (or calls of at most QR_CQ_FUSED_MAX_BATCH matrices at build time).
+#ifndef QR_CQ_FUSED_MAX_BATCH
+#define QR_CQ_FUSED_MAX_BATCH 0
+#endif
+bool cq_fused(int batch) {
+  if (const char* env = std::getenv("QR_CHOLQR_FUSED")) return env[0] == '1';
+  return batch <= QR_CQ_FUSED_MAX_BATCH;
+}
+
 // Workspace floats of the CholeskyQR2 route for `batch` matrices: Gram
 // partials, three 64 x 64 matrices per matrix, flags.
 size_t cq_workspace_floats(int batch) {
   int nc = (256 + batch - 1) / batch;
   if (nc > kCqMaxChunks) nc = kCqMaxChunks;
-  return (size_t)batch * nc * kCqSlot + (size_t)batch * 3 * kCqMat + (size_t)batch;
+  return (size_t)batch * nc * kCqSlot + (size_t)batch * 3 * kCqMat + 2 * (size_t)batch;
 }
 
-// The four launches of one block. Src / Hb point at the block's top-left
+// The three launches of one block. Src / Hb point at the block's top-left
 // element of matrix 0; ws holds cq_workspace_floats(batch) floats.
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
@@ -765,16 +832,25 @@ hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb
   float* part = ws;
   float* mats = part + (size_t)batch * ncw * kCqSlot;
   int* flags = reinterpret_cast<int*>(mats + (size_t)batch * 3 * kCqMat);
+  int* cnt = flags + batch;
   const int64_t sMb = 3 * kCqMat;
   const unsigned g1 = (unsigned)(nc * batch);
-  hipLaunchKernelGGL((k_cq_gram<false>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r, rc, nc,
-                     (const float*)mats, sMb, part, (const int*)flags);
-  hipLaunchKernelGGL(k_cq_chol1, dim3(batch), dim3(256), 0, stream, (const float*)part, nc, mats,
-                     sMb, flags);
-  hipLaunchKernelGGL((k_cq_gram<true>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r, rc, nc,
-                     (const float*)mats, sMb, part, (const int*)flags);
-  hipLaunchKernelGGL(k_cq_recon, dim3(batch), dim3(256), 0, stream, (const float*)part, nc, mats,
-                     sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
+  if (cq_fused(batch)) {
+    hipLaunchKernelGGL((k_cq_gram<false, true>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r,
+                       rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
+    hipLaunchKernelGGL((k_cq_gram<true, true>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r,
+                       rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
+  } else {
+    hipLaunchKernelGGL((k_cq_gram<false, false>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds,
+                       r, rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws,
+                       sTwb);
+    hipLaunchKernelGGL(k_cq_chol1, dim3(batch), dim3(256), 0, stream, (const float*)part, nc,
+                       mats, sMb, flags);
+    hipLaunchKernelGGL((k_cq_gram<true, false>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r,
+                       rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
+    hipLaunchKernelGGL(k_cq_recon, dim3(batch), dim3(256), 0, stream, (const float*)part, nc, mats,
+                       sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
+  }
   {
     int rc3 = 0, nc3 = 0;
     cq_chunks(r - kCqB, batch, 64, &rc3, &nc3);
@@ -782,6 +858,24 @@ hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb
                        lds, Hb, sHb, ldh, r, rc3, nc3, (const float*)mats, sMb,
                        (const int*)flags);
   }
+  return hipGetLastError();
+}
+
+__global__ void k_cq_zero(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Zero the per-matrix arrival counters of the workspace (once per call, before
+// its first launch_cq_block: the workspace arrives uninitialised; every use
+// leaves them at zero again).
+hipError_t launch_cq_reset(float* ws, int batch, hipStream_t stream) {
+  int ncw = (256 + batch - 1) / batch;
+  if (ncw > kCqMaxChunks) ncw = kCqMaxChunks;
+  int* cnt = reinterpret_cast<int*>(ws + (size_t)batch * ncw * kCqSlot +
+                                    (size_t)batch * 3 * kCqMat) + batch;
+  hipLaunchKernelGGL(k_cq_zero, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, stream, cnt,
+                     batch);
   return hipGetLastError();
 }
 
