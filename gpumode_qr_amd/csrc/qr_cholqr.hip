@@ -272,7 +272,9 @@ __device__ __forceinline__ void cq_inv_offdiag(const float* __restrict__ U, floa
     }
     __syncthreads();
   }
-  for (int e = threadIdx.x; e < 6 * 256; e += 256) {  // tiles (I, J), I > J
+#pragma unroll
+  for (int it = 0; it < 6; ++it) {
+    const int e = threadIdx.x + 256 * it;  // tiles (I, J), I > J
     const int t = e >> 8, el = e & 255;
     const int I = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3), J = t < 3 ? 0 : (t < 5 ? 1 : 2);
     Ri[(16 * I + (el >> 4)) * kCqLS + 16 * J + (el & 15)] = 0.0f;
@@ -324,7 +326,9 @@ __device__ __forceinline__ void cq_chol_inv_blocked(float* __restrict__ G, float
       }
     __syncthreads();
   }
-  for (int e = threadIdx.x; e < 6 * 256; e += 256) {  // lower blocks of R
+#pragma unroll
+  for (int it = 0; it < 6; ++it) {
+    const int e = threadIdx.x + 256 * it;  // lower blocks of R
     const int t = e >> 8, el = e & 255;
     const int I = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3), J = t < 3 ? 0 : (t < 5 ? 1 : 2);
     G[(16 * I + (el >> 4)) * kCqLS + 16 * J + (el & 15)] = 0.0f;
@@ -458,7 +462,9 @@ __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
     if (!dok) *dbad = 1;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < kCqMat; e += 256) {  // D^-1 G1 D^-1
+#pragma unroll
+  for (int it = 0; it < kCqMat / 256; ++it) {
+    const int e = threadIdx.x + 256 * it;  // D^-1 G1 D^-1
     const int i = e >> 6, c = e & 63;
     G[i * kCqLS + c] *= rdsc[i] * rdsc[c];
   }
@@ -467,7 +473,9 @@ __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
   float* M1 = mats + (int64_t)b * sMb;
   float* R1 = M1 + kCqMat;
   // R1 = R1s D, M1 = R1^-1 = D^-1 R1s^-1.
-  for (int e = threadIdx.x; e < kCqMat; e += 256) {
+#pragma unroll
+  for (int it = 0; it < kCqMat / 256; ++it) {
+    const int e = threadIdx.x + 256 * it;
     const int i = e >> 6, c = e & 63;
     R1[e] = G[i * kCqLS + c] * dsc[c];
     M1[e] = Ri[i * kCqLS + c] * rdsc[i];
@@ -532,7 +540,9 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   __syncthreads();
   {  // max |G2 - I| (NaN propagates)
     float dev = 0.0f;
-    for (int e = threadIdx.x; e < kCqMat; e += 256) {
+#pragma unroll
+    for (int it = 0; it < kCqMat / 256; ++it) {
+      const int e = threadIdx.x + 256 * it;
       const int i = e >> 6, c = e & 63;
       const float d = fabsf(G2[i * kCqLS + c] - ((i == c) ? 1.0f : 0.0f));
       dev = (d <= dev) ? dev : d;
@@ -603,7 +613,9 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   }
   // H's top 64 rows of the block: R = S R_c on and above the diagonal, L1 below.
   float* Hm = Hb + (int64_t)b * sHb;
-  for (int e = threadIdx.x; e < kCqMat; e += 256) {
+#pragma unroll
+  for (int it = 0; it < kCqMat / 256; ++it) {
+    const int e = threadIdx.x + 256 * it;
     const int i = e >> 6, c = e & 63;
     Hm[(int64_t)i * ldh + c] = (i <= c) ? sgn[i] * Rc[i * kCqLS + c] : At[i * kCqLS + c];
   }
