@@ -1,6 +1,7 @@
 """Run only the QR forward pass on one config's input, for profilers.
 
     python -m gpumode_qr_amd.profile_run --config 4 --calls 3
+    python -m gpumode_qr_amd.profile_run --shape 2x4096 --calls 3
 
 Unlike ``bench.py`` this runs no FP64 gates (they call torch's
 householder_product) and no torch.geqrf, so a ``rocprofv3 --pmc`` pass over it
@@ -10,6 +11,9 @@ launches the same kernels, so per-dispatch counters divide cleanly by call.
 Before the calls it runs one ``torch.neg(A, out=C)``: an elementwise kernel
 that reads ``batch * n * n * 4`` bytes and writes as many, the known-size
 transfer that calibrates FETCH_SIZE / WRITE_SIZE.
+
+``--shape BxN`` factors B seeded N(0,1) matrices of order N instead of a config
+(the official shapes' sizes, e.g. 2x4096).
 
 ``--layout colmajor`` passes the same matrices as a column-major view, which
 geqrf first copies into H with ``k_copy_in`` (with the row-major default the
@@ -25,6 +29,7 @@ import sys
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", type=int, default=4, help="1..5 (the benchmark configs)")
+    ap.add_argument("--shape", default=None, help="BxN: B seeded N(0,1) matrices of order N")
     ap.add_argument("--calls", type=int, default=3)
     ap.add_argument("--layout", choices=("rowmajor", "colmajor"), default="rowmajor",
                     help="colmajor: a column-major view of the same matrices (adds k_copy_in)")
@@ -38,8 +43,14 @@ def main(argv=None) -> int:
         print("profile_run needs a GPU", file=sys.stderr)
         return 1
     _lib.load()
-    prob = inputs.make_config_problem(args.config, device="cuda")
-    A = prob.tensor
+    if args.shape:
+        b_, n_ = (int(x) for x in args.shape.lower().split("x"))
+        g = torch.Generator().manual_seed(n_)
+        A = torch.randn(b_, n_, n_, generator=g).to("cuda")
+        prob = inputs.Problem(name=f"b{b_}_n{n_}_gauss", tensor=A, meta={})
+    else:
+        prob = inputs.make_config_problem(args.config, device="cuda")
+        A = prob.tensor
     if args.layout == "colmajor":
         A = A.transpose(-1, -2).contiguous().transpose(-1, -2)
     b, n = prob.batch, prob.n
