@@ -345,33 +345,41 @@ __device__ __forceinline__ void cq_lu_blocked(float* __restrict__ A, float* __re
                                               float* __restrict__ pinv, int w, int lane) {
   const int c = lane & 15, g = lane >> 4;
   for (int K = 0; K < 4; ++K) {
+    float* Ad = cq_tile_ptr(A, K, K);
     if (w == 0) {
-      float* Ad = cq_tile_ptr(A, K, K);
       float x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) x[i] = Ad[i * kCqLS + c];
       float sv = 1.0f, pi = 1.0f;
       cq_lu16(x, sv, pi, c);
-      float u[16], l[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        u[i] = (i <= c) ? x[i] : 0.0f;
-        l[i] = (i > c) ? x[i] : ((i == c) ? 1.0f : 0.0f);
-      }
-      float mu[16], ml[16];
-      cq_inv16_upper(mu, u, pi, c);
-      cq_inv16_unit_lower(ml, l, c);
       if (g == 0) {
-        float* Ud = cq_tile_ptr(Ui, K, K);
-        float* Ld = Li + 16 * K * kCqLS;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          Ad[i * kCqLS + c] = x[i];
-          Ud[i * kCqLS + c] = mu[i];
-          Ld[i * kCqLS + c] = ml[i];
-        }
+        for (int i = 0; i < 16; ++i) Ad[i * kCqLS + c] = x[i];
         sgn[16 * K + c] = sv;
         pinv[16 * K + c] = pi;
+      }
+    }
+    __syncthreads();
+    // The two triangular inverses of the diagonal block at once: U_KK^-1 in
+    // wave 0, L_KK^-1 in wave 1.
+    if (w < 2) {
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = Ad[i * kCqLS + c];
+      float m[16];
+      if (w == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = (i <= c) ? x[i] : 0.0f;
+        cq_inv16_upper(m, x, pinv[16 * K + c], c);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = (i > c) ? x[i] : ((i == c) ? 1.0f : 0.0f);
+        cq_inv16_unit_lower(m, x, c);
+      }
+      if (g == 0) {
+        float* D = (w == 0) ? cq_tile_ptr(Ui, K, K) : Li + 16 * K * kCqLS;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) D[i * kCqLS + c] = m[i];
       }
     }
     __syncthreads();
