@@ -642,9 +642,11 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
 // matrix b's nchunk workgroups to finish (counted in cnt[b], which it resets
 // to zero) then runs the per-matrix step: cq_chol1_body in pass 1,
 // cq_recon_body in pass 2. Partials are summed in chunk order, so the result
-// does not depend on which workgroup is last. Four waves, rc / 4 rows each.
+// does not depend on which workgroup is last. kCqGramWaves(kFused) waves,
+// rc / waves rows each (four when fused: the per-matrix bodies use 256 threads).
+__host__ __device__ constexpr int kCqGramWaves(bool fused) { return fused ? 4 : 8; }
 template <bool kPass2, bool kFused>
-__global__ __launch_bounds__(256) void k_cq_gram(const float* __restrict__ Src, int64_t sSb,
+__global__ __launch_bounds__(64 * kCqGramWaves(kFused)) void k_cq_gram(const float* __restrict__ Src, int64_t sSb,
                                                  int64_t lds, int r, int rc, int nchunk,
                                                  float* __restrict__ mats, int64_t sMb,
                                                  float* __restrict__ part,
@@ -652,12 +654,13 @@ __global__ __launch_bounds__(256) void k_cq_gram(const float* __restrict__ Src, 
                                                  float* __restrict__ Hb, int64_t sHb, int64_t ldh,
                                                  float* __restrict__ tau, int64_t sTaub,
                                                  float* __restrict__ Tws, int64_t sTwb) {
-  constexpr int kRed = 4 * kCqPart + 8;
+  constexpr int kNW = kCqGramWaves(kFused);
+  constexpr int kRed = kNW * kCqPart + 2 * kNW;
   constexpr int kLds = !kFused ? kRed
                                : (kPass2 ? kCqReconLds : (kCqChol1Lds > kRed ? kCqChol1Lds : kRed));
   __shared__ __attribute__((aligned(16))) float smem[kLds];
   float (*red)[kCqPart] = reinterpret_cast<float (*)[kCqPart]>(smem);
-  unsigned long long* wmask = reinterpret_cast<unsigned long long*>(smem + 4 * kCqPart);
+  unsigned long long* wmask = reinterpret_cast<unsigned long long*>(smem + kNW * kCqPart);
   __shared__ int last;
   const int b = blockIdx.x / nchunk;
   const int c = blockIdx.x - b * nchunk;
@@ -673,7 +676,7 @@ __global__ __launch_bounds__(256) void k_cq_gram(const float* __restrict__ Src, 
   float mr[40];
   if constexpr (kPass2) cq_load_mb(mr, mats + (int64_t)b * sMb, lane);
 
-  const int rw = rc >> 2;
+  const int rw = rc / kNW;
   const int rbeg = c * rc + w * rw;
   bool nz[4] = {false, false, false, false};  // pass 1: column 16I + k nonzero below row 64
   for (int t = 0; t < rw; t += 16) {
@@ -723,10 +726,17 @@ __global__ __launch_bounds__(256) void k_cq_gram(const float* __restrict__ Src, 
   }
   __syncthreads();
   float* dst = part + (int64_t)blockIdx.x * kCqSlot;
-  for (int e = threadIdx.x; e < kCqPart; e += 256)
-    dst[e] = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
-  if (!kPass2 && threadIdx.x == 0)
-    *reinterpret_cast<unsigned long long*>(dst + kCqPart) = wmask[0] | wmask[1] | wmask[2] | wmask[3];
+  for (int e = threadIdx.x; e < kCqPart; e += 64 * kNW) {
+    float sum = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+    if constexpr (kNW == 8) sum += (red[4][e] + red[5][e]) + (red[6][e] + red[7][e]);
+    dst[e] = sum;
+  }
+  if (!kPass2 && threadIdx.x == 0) {
+    unsigned long long m = 0;
+#pragma unroll
+    for (int u = 0; u < kNW; ++u) m |= wmask[u];
+    *reinterpret_cast<unsigned long long*>(dst + kCqPart) = m;
+  }
   if constexpr (!kFused) return;
   // Publish the partial, count it; the last workgroup of matrix b goes on.
   __threadfence();
@@ -802,14 +812,14 @@ __global__ __launch_bounds__(256) void k_cq_form(const float* __restrict__ Src, 
   }
 }
 
-// Rows per chunk (a multiple of 64) and chunk count for `rows` rows: about 256
-// workgroups over the batch, at most max_chunks per matrix.
-void cq_chunks(int rows, int batch, int max_chunks, int* rc, int* nchunk) {
+// Rows per chunk (a multiple of unit) and chunk count for `rows` rows: about
+// 256 workgroups over the batch, at most max_chunks per matrix.
+void cq_chunks(int rows, int batch, int max_chunks, int unit, int* rc, int* nchunk) {
   int nc = (256 + batch - 1) / batch;
   if (nc > max_chunks) nc = max_chunks;
   if (nc < 1) nc = 1;
-  int c = ((rows + nc - 1) / nc + 63) / 64 * 64;
-  if (c < 64) c = 64;
+  int c = ((rows + nc - 1) / nc + unit - 1) / unit * unit;
+  if (c < unit) c = unit;
   *rc = c;
   *nchunk = (rows + c - 1) / c;
 }
@@ -844,8 +854,10 @@ hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
                            int64_t sTwb, float* ws, int batch, hipStream_t stream) {
   if (r <= kCqB || r > kMaxStripRows || batch < 1) return hipErrorInvalidValue;
+  const bool fused = cq_fused(batch);
+  const int gw = kCqGramWaves(fused);
   int rc = 0, nc = 0;
-  cq_chunks(r, batch, kCqMaxChunks, &rc, &nc);
+  cq_chunks(r, batch, kCqMaxChunks, 16 * gw, &rc, &nc);
   int ncw = (256 + batch - 1) / batch;
   if (ncw > kCqMaxChunks) ncw = kCqMaxChunks;
   if (nc > ncw) return hipErrorInvalidValue;  // partials sized for ncw chunks
@@ -855,25 +867,25 @@ hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb
   int* cnt = flags + batch;
   const int64_t sMb = 3 * kCqMat;
   const unsigned g1 = (unsigned)(nc * batch);
-  if (cq_fused(batch)) {
+  if (fused) {
     hipLaunchKernelGGL((k_cq_gram<false, true>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r,
                        rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
     hipLaunchKernelGGL((k_cq_gram<true, true>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r,
                        rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
   } else {
-    hipLaunchKernelGGL((k_cq_gram<false, false>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds,
+    hipLaunchKernelGGL((k_cq_gram<false, false>), dim3(g1), dim3(64 * gw), 0, stream, Src, sSb, lds,
                        r, rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws,
                        sTwb);
     hipLaunchKernelGGL(k_cq_chol1, dim3(batch), dim3(256), 0, stream, (const float*)part, nc,
                        mats, sMb, flags);
-    hipLaunchKernelGGL((k_cq_gram<true, false>), dim3(g1), dim3(256), 0, stream, Src, sSb, lds, r,
+    hipLaunchKernelGGL((k_cq_gram<true, false>), dim3(g1), dim3(64 * gw), 0, stream, Src, sSb, lds, r,
                        rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
     hipLaunchKernelGGL(k_cq_recon, dim3(batch), dim3(256), 0, stream, (const float*)part, nc, mats,
                        sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
   }
   {
     int rc3 = 0, nc3 = 0;
-    cq_chunks(r - kCqB, batch, 64, &rc3, &nc3);
+    cq_chunks(r - kCqB, batch, 64, 64, &rc3, &nc3);
     hipLaunchKernelGGL(k_cq_form, dim3((unsigned)(nc3 * batch)), dim3(256), 0, stream, Src, sSb,
                        lds, Hb, sHb, ldh, r, rc3, nc3, (const float*)mats, sMb,
                        (const int*)flags);
