@@ -848,8 +848,8 @@ size_t cq_workspace_floats(int batch) {
   return (size_t)batch * nc * kCqSlot + (size_t)batch * 3 * kCqMat + 2 * (size_t)batch;
 }
 
-// The launches of one block: Gram 1, pass 1, Gram 2, pass 2 (the two pairs
-// fused into one launch each with cq_fused), then V. Src / Hb point at the block's top-left
+// The launches of one block: Gram 1, pass 1, Gram 2, pass 2 (each pair one
+// launch with cq_fused), then V. Src / Hb point at the block's top-left
 // element of matrix 0; ws holds cq_workspace_floats(batch) floats.
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
