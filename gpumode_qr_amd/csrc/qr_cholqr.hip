@@ -51,9 +51,13 @@ __host__ __device__ constexpr int cq_tile(int I, int J) {
   return I * 4 - I * (I - 1) / 2 + (J - I);
 }
 
+// Max over the wave; NaN if any lane holds NaN.
 __device__ __forceinline__ float wave_max64(float v) {
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+  for (int o = 1; o < 64; o <<= 1) {
+    const float u = __shfl_xor(v, o);
+    v = (v != v || u != u) ? __builtin_nanf("") : fmaxf(v, u);
+  }
   return v;
 }
 
@@ -97,8 +101,9 @@ __device__ __forceinline__ void cq_tile_times_m(f32x4 (&x)[4], const float* __re
 // The 64 x 64 Gram of matrix b from its nchunk partials into G (row stride
 // kCqLS), upper tiles mirrored. Every element has exactly one writer; the
 // chunks are summed in order, 10 tiles x 4 chunks of loads in flight.
-__device__ __forceinline__ void cq_sum_gram(float* __restrict__ G, const float* __restrict__ part,
-                                            int b, int nchunk) {
+// Returns this thread's max |G - I| over its elements (NaN propagates).
+__device__ __forceinline__ float cq_sum_gram(float* __restrict__ G, const float* __restrict__ part,
+                                             int b, int nchunk) {
   const int e = threadIdx.x;  // 256 threads: element e of every tile
   const int ti = e >> 4, tj = e & 15;
   const float* src = part + (int64_t)b * nchunk * kCqSlot + e;
@@ -117,6 +122,7 @@ __device__ __forceinline__ void cq_sum_gram(float* __restrict__ G, const float* 
 #pragma unroll
       for (int t = 0; t < kCqTiles; ++t) s[t] += v[u][t];
   }
+  float dev = 0.0f;
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -124,7 +130,10 @@ __device__ __forceinline__ void cq_sum_gram(float* __restrict__ G, const float* 
       const float sv = s[cq_tile(I, J)];
       G[(16 * I + ti) * kCqLS + 16 * J + tj] = sv;
       if (I != J) G[(16 * J + tj) * kCqLS + 16 * I + ti] = sv;
+      const float d = fabsf(sv - ((I == J && ti == tj) ? 1.0f : 0.0f));
+      dev = (d <= dev) ? dev : d;
     }
+  return dev;
 }
 
 // ---------------------------------------------------------------------------
@@ -536,7 +545,10 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   const float* M1g = mats + (int64_t)b * sMb;
   const float* S = Src + (int64_t)b * sSb;
 
-  cq_sum_gram(G2, part, b, nchunk);
+  {
+    const float dev = wave_max64(cq_sum_gram(G2, part, b, nchunk));  // max |G2 - I|
+    if (lane == 0) devw[w] = dev;
+  }
 #pragma unroll
   for (int it = 0; it < kCqMat / 256; ++it) {
     const int e = threadIdx.x + 256 * it;
@@ -546,24 +558,12 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
     At[i * kCqLS + c] = S[(int64_t)i * lds + c];
   }
   __syncthreads();
-  {  // max |G2 - I| (NaN propagates)
-    float dev = 0.0f;
-#pragma unroll
-    for (int it = 0; it < kCqMat / 256; ++it) {
-      const int e = threadIdx.x + 256 * it;
-      const int i = e >> 6, c = e & 63;
-      const float d = fabsf(G2[i * kCqLS + c] - ((i == c) ? 1.0f : 0.0f));
-      dev = (d <= dev) ? dev : d;
-    }
-    dev = wave_max64(dev);
-    if (lane == 0) devw[w] = dev;
-  }
-  __syncthreads();
   cq_chol_inv_blocked(G2, R2i, piv, w, lane);
   if (threadIdx.x < 64) {
-    const float dev = fmaxf(fmaxf(devw[0], devw[1]), fmaxf(devw[2], devw[3]));
-    const bool ok = __all(piv[threadIdx.x] >= 0.25f && piv[threadIdx.x] <= 4.0f) &&
-                    dev <= kCqOrthTol && !(dev != dev);
+    // Every devw[u] <= tol (false for NaN).
+    const bool dok = devw[0] <= kCqOrthTol && devw[1] <= kCqOrthTol &&
+                     devw[2] <= kCqOrthTol && devw[3] <= kCqOrthTol;
+    const bool ok = __all(piv[threadIdx.x] >= 0.25f && piv[threadIdx.x] <= 4.0f) && dok;
     if (threadIdx.x == 0) okflag = ok ? 1 : 0;
   }
   __syncthreads();
