@@ -375,7 +375,8 @@ def test_side_stream_and_strided_input_bitwise():
 def test_concurrent_host_threads_bitwise():
     """Two host threads, each on its own stream, factor different matrices at
     the same time. Both calls use the library's shared look-ahead stream
-    (n > 128). Every result equals the one of a lone call, bit for bit."""
+    (n > 128), and the b8 n700 calls take the CholeskyQR2 route for their first
+    three outer blocks. Every result equals the one of a lone call, bit for bit."""
     import threading
 
     _say("two host threads, two streams, shared look-ahead stream")
