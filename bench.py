@@ -53,8 +53,8 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
 # Measured HBM MiB (read + write) per geqrf call of each kernel family, per
 # config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
-# ``python -m gpumode_qr_amd.profile_run --config C --calls 3`` (cfg 5 and the
-# CholeskyQR2 route: profiles/qr_cholqr_route_hbm_traffic_mfma_lds.md), each scaled by
+# ``python -m gpumode_qr_amd.profile_run --config C --calls 3`` (cfg 5 measured
+# after the CholeskyQR2 route took over its large blocks), each scaled by
 # the same counter's reading for a known-size elementwise kernel that
 # profile_run runs first (FETCH x2.000, WRITE x1.000). Counters cannot be read
 # from inside this process; rerun those commands after changing a kernel.
