@@ -684,3 +684,31 @@ def test_cholqr_exact_zero_structure(monkeypatch, oracle, kind):
     if kind == "upper":
         assert torch.equal(tau, torch.zeros_like(tau))
         assert torch.equal(H, A)
+
+
+@pytest.mark.parametrize("n,batch", [(300, 3), (700, 5)])
+def test_cholqr_fused_variant(monkeypatch, oracle, n, batch):
+    """The fused Gram + per-matrix kernels (QR_CHOLQR_FUSED=1: the last
+    workgroup of a matrix to finish runs its per-matrix step, whichever it is)
+    match the oracle, and each variant is bit-identical with look-ahead on and
+    off. The two variants split the Gram rows over different wave counts, so
+    they round differently from each other."""
+    _say(f"cholqr fused and separate kernels n={n} b={batch}")
+    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
+    A = _gauss(batch, n, seed=n + 9)
+    A[1, :, 100] = 0.0  # one matrix takes the fallback panels in one block
+    Ad = A.to(DEV)
+    out = {}
+    for fused in ("0", "1"):
+        for la in ("0", "1"):
+            monkeypatch.setenv("QR_CHOLQR_FUSED", fused)
+            monkeypatch.setenv("QR_LOOKAHEAD", la)
+            out[fused, la] = hip_qr.geqrf(Ad)
+    torch.cuda.synchronize()
+    for fused in ("0", "1"):
+        (H0, t0), (H1, t1) = out[fused, "0"], out[fused, "1"]
+        assert torch.equal(H0, H1) and torch.equal(t0, t1), fused
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    H, tau = out["1", "1"]
+    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
+                  what=f"fused n={n}")
