@@ -375,7 +375,7 @@ __device__ __forceinline__ void panel_factor(PanelShared<NW, RL>& sh, int b, flo
 // Writes V_p / R in place, tau_p, and T_p at Tb + 256 p. The panel's columns are
 // read from H, or from A (row stride lda, unit column stride) when A is not
 // null: the first outer block reads the caller's matrix directly. When `only`
-// is not null, only matrices b with only[b] != 0 are factored (the others
+// is not null, only matrices b with only[b] == 1 are factored (the others
 // return at once).
 template <int NW, int RL>
 __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
@@ -386,12 +386,12 @@ __global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_
                                                    const int* __restrict__ only) {
   __shared__ PanelShared<NW, RL> sh;
   const int b = blockIdx.x;
-  if (only && only[b] == 0) return;  // this matrix's block was factored elsewhere
+  if (only && only[b] != 1) return;  // this matrix's block was factored elsewhere
   panel_factor<NW, RL>(sh, b, H, sHb, ldh, J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda);
 }
 
 // Panels 0..nblk-1 of the outer block, one after the other in one workgroup
-// per matrix, for the matrices b with only[b] != 0 (the others return at
+// per matrix, for the matrices b with only[b] == 1 (the others return at
 // once). Panel p + 1 reads V_p, T_p from global memory after the workgroup
 // barrier that ends panel p.
 template <int NW, int RL>
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(64 * NW) void k_panel_seq(float* __restrict__ H, in
                                                        const int* __restrict__ only) {
   __shared__ PanelShared<NW, RL> sh;
   const int b = blockIdx.x;
-  if (only[b] == 0) return;
+  if (only[b] != 1) return;
   for (int p = 0; p < nblk; ++p) {
     const int kw = (r - 16 * p) < 16 ? (r - 16 * p) : 16;
     panel_factor<NW, RL>(sh, b, H, sHb, ldh, J0, p, r, kw, tau, sTaub, Tws, sTwb, A, sAb, lda);

@@ -46,6 +46,12 @@ constexpr float kCqGramMin = 1e-30f;
 constexpr float kCqGramMax = 1e30f;
 constexpr float kCqPivMin = 1e-5f;
 constexpr float kCqOrthTol = 1e-2f;
+constexpr float kCqSingleMaxF2 = 144.0f;  // ||R1s^-1||_F^2 bound of the one-pass route
+// Per-matrix flags of a block: the route with two passes, with one, or the
+// Householder panels.
+constexpr int kCqFlagTwo = 0;
+constexpr int kCqFlagFallback = 1;
+constexpr int kCqFlagSingle = 2;
 
 __host__ __device__ constexpr int cq_tile(int I, int J) {
   return I * 4 - I * (I - 1) / 2 + (J - I);
@@ -452,18 +458,21 @@ __device__ __forceinline__ void cq_store_rows(float* __restrict__ Z, int64_t ldz
 
 // ---------------------------------------------------------------------------
 // Pass 1 per matrix: scaled Cholesky of G1, guard, M1 = R1^-1 and R1 into the
-// workspace (mats[b]: M1 at 0, R1 at kCqMat), flag[b] = 0 (ok) or 1.
-constexpr int kCqChol1Lds = 2 * kCqB * kCqLS + 4 * 64;  // floats
+// workspace (mats[b]: M1 at 0, R1 at kCqMat), flag[b] = kCqFlagTwo,
+// kCqFlagSingle (one pass is enough; only with allow_single) or
+// kCqFlagFallback.
+constexpr int kCqChol1Lds = 2 * kCqB * kCqLS + 4 * 64 + 16;  // floats
 __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
                                               const float* __restrict__ part, int nchunk,
                                               float* __restrict__ mats, int64_t sMb,
-                                              int* __restrict__ flags) {
+                                              int* __restrict__ flags, bool allow_single) {
   float* const G = smem;
   float* const Ri = G + kCqB * kCqLS;
   float* const piv = Ri + kCqB * kCqLS;
   float* const dsc = piv + 64;   // d_j = sqrt(G1_jj)
   float* const rdsc = dsc + 64;  // 1 / d_j
   int* const dbad = reinterpret_cast<int*>(rdsc + 64);
+  float* const ssw = rdsc + 68;  // per-wave sums of squares of R1s^-1
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   cq_sum_gram(G, part, b, nchunk);
@@ -490,13 +499,20 @@ __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
   float* M1 = mats + (int64_t)b * sMb;
   float* R1 = M1 + kCqMat;
   // R1 = R1s D, M1 = R1^-1 = D^-1 R1s^-1.
+  float ss = 0.0f;
 #pragma unroll
   for (int it = 0; it < kCqMat / 256; ++it) {
     const int e = threadIdx.x + 256 * it;
     const int i = e >> 6, c = e & 63;
+    const float ri = Ri[i * kCqLS + c];
     R1[e] = G[i * kCqLS + c] * dsc[c];
-    M1[e] = Ri[i * kCqLS + c] * rdsc[i];
+    M1[e] = ri * rdsc[i];
+    ss = fmaf(ri, ri, ss);
   }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+  if (lane == 0) ssw[w] = ss;
+  __syncthreads();
   if (threadIdx.x < 64) {
     const int j = threadIdx.x;
     unsigned long long nzm = 0;
@@ -505,7 +521,13 @@ __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
           part + ((int64_t)b * nchunk + c) * kCqSlot + kCqPart);
     const bool ok = __all(piv[j] >= kCqPivMin && piv[j] <= 3.0e38f) && *dbad == 0 &&
                     nzm == ~0ull;
-    if (j == 0) flags[b] = ok ? 0 : 1;
+    // One pass is enough when kappa(R1s) <= ||R1s||_F ||R1s^-1||_F = 8 ||R1s^-1||_F
+    // (unit columns) is at most 96: Q1 = A_b M1 is then orthonormal to about
+    // kappa^2 times the Gram's rounding (below 4e-5), as close as the second
+    // pass would make it for the (V, tau, R) it feeds.
+    const float ssum = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
+    const bool single = allow_single && ssum <= kCqSingleMaxF2;
+    if (j == 0) flags[b] = ok ? (single ? kCqFlagSingle : kCqFlagTwo) : kCqFlagFallback;
   }
 }
 
@@ -544,8 +566,17 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   int& okflag = *okflagp;
   const float* M1g = mats + (int64_t)b * sMb;
   const float* S = Src + (int64_t)b * sSb;
+  const bool single = flags[b] == kCqFlagSingle;  // no second pass: R2 = I
 
-  {
+  if (single) {
+#pragma unroll
+    for (int it = 0; it < kCqMat / 256; ++it) {
+      const int e = threadIdx.x + 256 * it;
+      const int i = e >> 6, c = e & 63;
+      G2[i * kCqLS + c] = (i == c) ? 1.0f : 0.0f;
+      R2i[i * kCqLS + c] = (i == c) ? 1.0f : 0.0f;
+    }
+  } else {
     const float dev = wave_max64(cq_sum_gram(G2, part, b, nchunk));  // max |G2 - I|
     if (lane == 0) devw[w] = dev;
   }
@@ -558,17 +589,21 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
     At[i * kCqLS + c] = S[(int64_t)i * lds + c];
   }
   __syncthreads();
-  cq_chol_inv_blocked(G2, R2i, piv, w, lane);
-  if (threadIdx.x < 64) {
-    // Every devw[u] <= tol (false for NaN).
-    const bool dok = devw[0] <= kCqOrthTol && devw[1] <= kCqOrthTol &&
-                     devw[2] <= kCqOrthTol && devw[3] <= kCqOrthTol;
-    const bool ok = __all(piv[threadIdx.x] >= 0.25f && piv[threadIdx.x] <= 4.0f) && dok;
-    if (threadIdx.x == 0) okflag = ok ? 1 : 0;
+  if (single) {
+    if (threadIdx.x == 0) okflag = 1;
+  } else {
+    cq_chol_inv_blocked(G2, R2i, piv, w, lane);
+    if (threadIdx.x < 64) {
+      // Every devw[u] <= tol (false for NaN).
+      const bool dok = devw[0] <= kCqOrthTol && devw[1] <= kCqOrthTol &&
+                       devw[2] <= kCqOrthTol && devw[3] <= kCqOrthTol;
+      const bool ok = __all(piv[threadIdx.x] >= 0.25f && piv[threadIdx.x] <= 4.0f) && dok;
+      if (threadIdx.x == 0) okflag = ok ? 1 : 0;
+    }
   }
   __syncthreads();
   if (!okflag) {
-    if (threadIdx.x == 0) flags[b] = 1;
+    if (threadIdx.x == 0) flags[b] = kCqFlagFallback;
     return;
   }
   {
@@ -593,7 +628,7 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   }
   __syncthreads();
   if (!okflag) {
-    if (threadIdx.x == 0) flags[b] = 1;
+    if (threadIdx.x == 0) flags[b] = kCqFlagFallback;
     return;
   }
   // M = Rinv U^-1 for the rows below the top block.
@@ -664,7 +699,7 @@ __global__ __launch_bounds__(64 * kCqGramWaves(kFused)) void k_cq_gram(const flo
   __shared__ int last;
   const int b = blockIdx.x / nchunk;
   const int c = blockIdx.x - b * nchunk;
-  if (kPass2 && flags[b] != 0) return;
+  if (kPass2 && flags[b] != kCqFlagTwo) return;  // fallback, or one pass is enough
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int k = lane & 15, g = lane >> 4;
@@ -750,7 +785,7 @@ __global__ __launch_bounds__(64 * kCqGramWaves(kFused)) void k_cq_gram(const flo
     cq_recon_body(smem, b, part, nchunk, mats, sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau,
                   sTaub, Tws, sTwb);
   else
-    cq_chol1_body(smem, b, part, nchunk, mats, sMb, flags);
+    cq_chol1_body(smem, b, part, nchunk, mats, sMb, flags, false);  // two passes
 }
 
 // The per-matrix steps as kernels of their own (one workgroup per matrix),
@@ -759,7 +794,7 @@ __global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part
                                                   float* __restrict__ mats, int64_t sMb,
                                                   int* __restrict__ flags) {
   __shared__ __attribute__((aligned(16))) float smem[kCqChol1Lds + 8];
-  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags);
+  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, true);
 }
 
 __global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part, int nchunk,
@@ -771,7 +806,7 @@ __global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part
                                                   float* __restrict__ tau, int64_t sTaub,
                                                   float* __restrict__ Tws, int64_t sTwb) {
   __shared__ __attribute__((aligned(16))) float smem[kCqReconLds];
-  if (flags[blockIdx.x] != 0) return;
+  if (flags[blockIdx.x] == kCqFlagFallback) return;
   cq_recon_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, Src, sSb, lds, Hb, sHb, ldh,
                 tau, sTaub, Tws, sTwb);
 }
@@ -785,7 +820,7 @@ __global__ __launch_bounds__(256) void k_cq_form(const float* __restrict__ Src, 
                                                  int64_t sMb, const int* __restrict__ flags) {
   const int b = blockIdx.x / nchunk;
   const int c = blockIdx.x - b * nchunk;
-  if (flags[b] != 0) return;
+  if (flags[b] == kCqFlagFallback) return;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int k = lane & 15, g = lane >> 4;

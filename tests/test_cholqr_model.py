@@ -90,8 +90,17 @@ def _signed_lu_blocked(Q, nb=16):
     return np.tril(A, -1) + np.eye(b, dtype=F32), np.triu(A), S
 
 
-def cq_block(Ab, flip=False, blocked=False):
-    """(H block, tau, T) of an r x 64 block by the route's steps."""
+def one_pass_ok(Ab):
+    """The kernel's test for skipping the second pass: ||R1s^-1||_F^2 <= 144,
+    i.e. kappa(R1s) <= 8 ||R1s^-1||_F <= 96 for unit-norm columns."""
+    G1 = (Ab.T @ Ab).astype(F32)
+    d = np.sqrt(np.diag(G1)).astype(F32)
+    R1s = _chol_upper((G1 / np.outer(d, d)).astype(F32))
+    return float((_inv_upper(R1s).astype(np.float64) ** 2).sum()) <= 144.0
+
+
+def cq_block(Ab, flip=False, blocked=False, passes=2):
+    """(H block, tau, T) of an r x 64 block by the route's steps (passes=1: R2 = I)."""
     r, b = Ab.shape
     G1 = (Ab.T @ Ab).astype(F32)
     d = np.sqrt(np.diag(G1)).astype(F32)
@@ -99,7 +108,7 @@ def cq_block(Ab, flip=False, blocked=False):
     R1 = (R1s * d[None, :]).astype(F32)
     M1 = (_inv_upper(R1s) / d[:, None]).astype(F32)
     X = (Ab @ M1).astype(F32)
-    R2 = _chol_upper((X.T @ X).astype(F32))
+    R2 = _chol_upper((X.T @ X).astype(F32)) if passes == 2 else np.eye(b, dtype=F32)
     Rinv = (M1 @ _inv_upper(R2)).astype(F32)
     Rc = (R2 @ R1).astype(F32)
     Qt = (Ab[:b] @ Rinv).astype(F32)
@@ -145,6 +154,22 @@ def test_route_matches_lapack_sgeqrf(kind, r, blocked):
     kappa = 100.0 if kind == "cond1e2" else 1.0
     tol = tolerance(r) * max(1.0, kappa / 10.0)
     assert max(_errors(Ab, H, tau, Hr, taur)) <= tol
+
+
+@pytest.mark.parametrize("r", [512, 2048, 4096])
+def test_one_pass_route_matches_lapack(r):
+    """Blocks that pass the one-pass test: CholeskyQR with a single pass gives
+    the same (V, tau, R) as LAPACK within the tolerance, like two passes."""
+    Ab = _block("gauss", r, seed=r + 1)
+    assert one_pass_ok(Ab)
+    H, tau, _ = cq_block(Ab, passes=1)
+    Hr, taur, _, _ = lapack.sgeqrf(Ab)
+    assert max(_errors(Ab, H, tau, Hr, taur)) <= tolerance(r)
+
+
+def test_one_pass_test_rejects_ill_conditioned_block():
+    Ab = _block("cond1e2", 512, seed=9)  # kappa = 100 inside the block
+    assert not one_pass_ok(Ab)
 
 
 def test_route_matches_oracle(oracle):
