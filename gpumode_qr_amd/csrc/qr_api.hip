@@ -75,24 +75,19 @@ size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kTStride * sizeof
 size_t ws_cq_bytes(int batch) { return align_up(qr::cq_workspace_floats(batch) * sizeof(float)); }
 
 // Outer blocks of 64 columns with at least this many rows take the CholeskyQR2
-// route: by default only in calls of at most kCqMaxBatch matrices, where the
-// Householder panels' column steps are the critical path. QR_CHOLQR=0
-// switches the route off, QR_CHOLQR=1 allows it at any batch size,
-// QR_CHOLQR_MIN_ROWS overrides the row bound (the route needs r > 64).
-constexpr int kCqMaxBatch = 16;
+// route: 256 rows in calls of at most 64 matrices, 512 above (with many
+// matrices the Householder panels of short blocks are throughput-bound and
+// cheaper). QR_CHOLQR=0 switches the route off; QR_CHOLQR_MIN_ROWS overrides
+// the bound (the route needs r > 64).
 int cq_min_rows(int batch) {
-  bool any_batch = false;
-  if (const char* env = std::getenv("QR_CHOLQR")) {
+  if (const char* env = std::getenv("QR_CHOLQR"))
     if (env[0] == '0') return 1 << 30;
-    any_batch = env[0] == '1';
-  }
   if (const char* env = std::getenv("QR_CHOLQR_MIN_ROWS")) {
     const int v = std::atoi(env);
     if (v >= 64) return v > 64 ? v : 65;
   }
-  return (any_batch || batch <= kCqMaxBatch) ? 512 : 1 << 30;
+  return batch <= 64 ? 256 : 512;
 }
-
 
 // Panels per outer block for size n (QR_OUTER_BLOCKS=1..8 overrides).
 int outer_blocks(int n) {
