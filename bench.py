@@ -53,19 +53,19 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 
 # Measured HBM MiB (read + write) per geqrf call of each kernel family, per
 # config: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
-# ``python -m gpumode_qr_amd.profile_run --config C --calls 3`` (cfg 5 measured
-# after the CholeskyQR2 route took over its large blocks), each scaled by
+# ``python -m gpumode_qr_amd.profile_run --config C --calls 3`` (cfgs 3-5 with
+# the CholeskyQR2 route at its default thresholds), each scaled by
 # the same counter's reading for a known-size elementwise kernel that
 # profile_run runs first (FETCH x2.000, WRITE x1.000). Counters cannot be read
 # from inside this process; rerun those commands after changing a kernel.
 HBM_MIB_PER_CALL = {
     "smalln": {2: 32.9 + 32.8},
-    # cfg 5: k_panel (blocks of < 512 rows) + k_panel_seq (fallback panels of
-    # the CholeskyQR2 route), both traced as "panel".
-    "panel": {3: 1534.2 + 381.3, 4: 459.9 + 140.2, 5: (31.5 + 5.3) + (7.5 + 3.5)},
-    "trail": {3: 2491.1 + 1697.2, 4: 1806.7 + 1443.8, 5: 3254.7 + 2809.2},
+    # k_panel + k_panel_seq (fallback panels of the CholeskyQR2 route), both
+    # traced as "panel".
+    "panel": {3: 1150.1 + 298.6, 4: 23.3 + 6.8, 5: 13.9 + 5.2},
+    "trail": {3: 2488.6 + 1698.1, 4: 1806.9 + 1433.4, 5: 3254.9 + 2809.5},
     # k_cq_gram + k_cq_chol1 + k_cq_recon + k_cq_form of the CholeskyQR2 route.
-    "cholqr": {5: (287.7 + 53.3 + 81.1 + 154.0) + (95.6 + 12.5 + 13.9 + 116.1)},
+    "cholqr": {3: 194.9 + 119.0, 4: 361.1 + 200.1, 5: 379.7 + 193.3},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
