@@ -568,15 +568,7 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   const float* S = Src + (int64_t)b * sSb;
   const bool single = flags[b] == kCqFlagSingle;  // no second pass: R2 = I
 
-  if (single) {
-#pragma unroll
-    for (int it = 0; it < kCqMat / 256; ++it) {
-      const int e = threadIdx.x + 256 * it;
-      const int i = e >> 6, c = e & 63;
-      G2[i * kCqLS + c] = (i == c) ? 1.0f : 0.0f;
-      R2i[i * kCqLS + c] = (i == c) ? 1.0f : 0.0f;
-    }
-  } else {
+  if (!single) {
     const float dev = wave_max64(cq_sum_gram(G2, part, b, nchunk));  // max |G2 - I|
     if (lane == 0) devw[w] = dev;
   }
@@ -606,17 +598,21 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
     if (threadIdx.x == 0) flags[b] = kCqFlagFallback;
     return;
   }
-  {
+  // With one pass R2 = I: Rinv = M1 and R_c = R1, already in LDS (and not
+  // overwritten below).
+  const float* const RinvP = single ? M1l : Rinv;
+  const float* const RcP = single ? R1l : Rc;
+  if (!single) {
     f32x4 acc[4];
     cq_mm64<true, true>(acc, M1l, R2i, w, lane);
     cq_store_rows(Rinv, kCqLS, acc, w, lane);
     cq_mm64<true, true>(acc, G2, R1l, w, lane);
     cq_store_rows(Rc, kCqLS, acc, w, lane);
+    __syncthreads();
   }
-  __syncthreads();
   {
     f32x4 acc[4];
-    cq_mm64<false, true>(acc, At, Rinv, w, lane);
+    cq_mm64<false, true>(acc, At, RinvP, w, lane);
     cq_store_rows(At, kCqLS, acc, w, lane);  // Q_top (each wave its own rows)
   }
   __syncthreads();
@@ -634,7 +630,7 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   // M = Rinv U^-1 for the rows below the top block.
   {
     f32x4 acc[4];
-    cq_mm64<true, true>(acc, Rinv, R2i, w, lane);
+    cq_mm64<true, true>(acc, RinvP, R2i, w, lane);
     cq_store_rows(mats + (int64_t)b * sMb + 2 * kCqMat, kCqB, acc, w, lane);
   }
   // T_qq = -U_qq S_q (L_qq^-1)^T for panel q = w: A operand U[i][q'] S[q'] (upper
@@ -660,7 +656,7 @@ __device__ __forceinline__ void cq_recon_body(float* __restrict__ smem, int b,
   for (int it = 0; it < kCqMat / 256; ++it) {
     const int e = threadIdx.x + 256 * it;
     const int i = e >> 6, c = e & 63;
-    Hm[(int64_t)i * ldh + c] = (i <= c) ? sgn[i] * Rc[i * kCqLS + c] : At[i * kCqLS + c];
+    Hm[(int64_t)i * ldh + c] = (i <= c) ? sgn[i] * RcP[i * kCqLS + c] : At[i * kCqLS + c];
   }
   if (threadIdx.x < 64) {
     const int i = threadIdx.x;
