@@ -174,7 +174,7 @@ def cpu_baseline(cfgs: list[int], torch) -> dict:
     torch.set_num_threads(cores)
     per_cfg = {}
     for cfg in cfgs:
-        spec = inputs.CONFIGS[cfg - 1]
+        spec = inputs.config_spec(cfg)
         A = inputs.config_tensor(spec)
         k = min(CPU_SAMPLE.get(cfg, 1), A.shape[0])
         sample = A[:k].contiguous()

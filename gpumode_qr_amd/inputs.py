@@ -161,8 +161,16 @@ def _config_tensor(spec: dict) -> torch.Tensor:
     return A
 
 
+def config_spec(cfg: int) -> dict:
+    """The workload whose ``"cfg"`` number is ``cfg`` (1-5)."""
+    for spec in CONFIGS:
+        if spec["cfg"] == cfg:
+            return spec
+    raise KeyError(f"no workload numbered {cfg}")
+
+
 def make_config_problem(cfg: int, device: str | torch.device = "cuda") -> Problem:
-    spec = CONFIGS[cfg - 1]
+    spec = config_spec(cfg)
     return Problem(name=spec["name"], tensor=config_tensor(spec).to(device), meta=dict(spec))
 
 

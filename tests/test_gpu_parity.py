@@ -272,7 +272,7 @@ def test_stress_suite_gates(n):
 
 def test_config1_parity_and_gates(oracle):
     _say("config 1 (b64 n32)")
-    A = inputs.config_tensor(inputs.CONFIGS[0])
+    A = inputs.config_tensor(inputs.config_spec(1))
     H, tau = _run(A)
     assert checker.check(A, H, tau).passed
     H_ref, tau_ref = oracle.geqrf(A.numpy())
@@ -283,7 +283,7 @@ def test_config1_parity_and_gates(oracle):
 
 def test_config2_parity_and_gates(oracle):
     _say("config 2 (b2048 n64)")
-    A = inputs.config_tensor(inputs.CONFIGS[1])
+    A = inputs.config_tensor(inputs.config_spec(2))
     H, tau = _run(A)
     assert checker.check(A, H, tau).passed
     H_ref, tau_ref = oracle.geqrf(A.numpy())
@@ -292,7 +292,7 @@ def test_config2_parity_and_gates(oracle):
 
 def test_config4_gates_and_sampled_parity(oracle):
     _say("config 4 (b64 n1024)")
-    A = inputs.config_tensor(inputs.CONFIGS[3])
+    A = inputs.config_tensor(inputs.config_spec(4))
     H, tau = _run(A)
     assert checker.check(A, H, tau).passed
     idx = [0, 37]
@@ -302,7 +302,7 @@ def test_config4_gates_and_sampled_parity(oracle):
 
 def test_config5_gates_and_gaussian_half_parity(oracle):
     _say("config 5 (b16 n2048)")
-    A = inputs.config_tensor(inputs.CONFIGS[4])
+    A = inputs.config_tensor(inputs.config_spec(5))
     H, tau = _run(A)
     assert torch.isfinite(H).all() and torch.isfinite(tau).all()
     res = checker.check(A, H, tau)
@@ -316,7 +316,7 @@ def test_config5_gates_and_gaussian_half_parity(oracle):
 
 def test_config3_gates_sampled():
     _say("config 3 (b640 n512), first 64 matrices")
-    A = inputs.config_tensor(inputs.CONFIGS[2])[:64]
+    A = inputs.config_tensor(inputs.config_spec(3))[:64]
     H, tau = _run(A)
     res = checker.check(A, H, tau)
     assert res.passed, res.as_dict()
