@@ -75,7 +75,7 @@ size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kTStride * sizeof
 size_t ws_cq_bytes(int batch) { return align_up(qr::cq_workspace_floats(batch) * sizeof(float)); }
 
 // Outer blocks of 64 columns with at least this many rows take the CholeskyQR2
-// route: 256 rows in calls of at most 64 matrices, 512 above (with many
+// route: 128 rows in calls of at most 64 matrices, 512 above (with many
 // matrices the Householder panels of short blocks are throughput-bound and
 // cheaper). QR_CHOLQR=0 switches the route off; QR_CHOLQR_MIN_ROWS overrides
 // the bound (the route needs r > 64).
@@ -86,7 +86,7 @@ int cq_min_rows(int batch) {
     const int v = std::atoi(env);
     if (v >= 64) return v > 64 ? v : 65;
   }
-  return batch <= 64 ? 256 : 512;
+  return batch <= 64 ? 128 : 512;
 }
 
 // Panels per outer block for size n (QR_OUTER_BLOCKS=1..8 overrides).

@@ -58,7 +58,7 @@ size_t qr_geqrf_f32_workspace(int batch, int n);
  * Full factorisation, replacing the champion variant's forward pass
  * (reference src/qrbench/variants.py:876-917 -> :761-805 for n > 128 and
  * :698-758 for n <= 128; baseline torch.geqrf at src/qrbench/reference.py:18-20).
- * Outer blocks of >= 256 rows (calls of at most 64 matrices; >= 512 rows above)
+ * Outer blocks of >= 128 rows (calls of at most 64 matrices; >= 512 rows above)
  * are factored by CholeskyQR2 with Householder reconstruction (the CholeskyQR
  * route of references/nvidia_winner_sol_combo.md:1051-1052), with the same
  * (V, tau, R) output; matrices it cannot factor to that standard take the
