@@ -256,6 +256,8 @@ def main() -> int:
     from gpumode_qr_amd import _lib, bench
 
     _lib.load()
+    route = _lib.default_options().as_dict()  # what every timed call runs with
+    print(f"[bench] route options: {route}", flush=True)
     cfgs = [int(c) for c in args.configs.split(",") if c.strip()]
     trace_kernels = ["smalln", "panel", "trail", "copy", "cholqr"]
     rows = [run_config(c, args.steps, args.warmup, torch, trace_kernels, not args.no_orgqr)
@@ -352,6 +354,7 @@ def main() -> int:
                 for r in rows
             ],
             "all_gates_pass": all(r["gates_pass"] for r in rows),
+            "route_options": route,
         },
         "roofline": roof,
         "cpu_baseline": cpu,

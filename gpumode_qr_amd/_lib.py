@@ -15,6 +15,23 @@ from pathlib import Path
 DEFAULT_LIB_PATH = Path(__file__).resolve().parent / "libqr_gfx950.so"
 LIB_PATH = Path(os.environ.get("QR_GFX950_LIB") or DEFAULT_LIB_PATH)
 
+
+class Options(ctypes.Structure):
+    """struct qr_options of include/qr_gfx950.h (route and schedule choices)."""
+
+    _fields_ = [
+        ("cholqr", ctypes.c_int),
+        ("cholqr_min_rows", ctypes.c_int),
+        ("cholqr_one_pass", ctypes.c_int),
+        ("cholqr_fused", ctypes.c_int),
+        ("lookahead", ctypes.c_int),
+        ("outer_panels", ctypes.c_int),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
 # Every symbol include/qr_gfx950.h declares, with (restype, argtypes).
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -30,6 +47,13 @@ SIGNATURES: dict[str, tuple] = {
         _int,
         [_ptr, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr, _size, _ptr],
     ),
+    "qr_default_options": (None, [ctypes.POINTER(Options)]),
+    "qr_geqrf_f32_ex": (
+        _int,
+        [_ptr, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr, _size, ctypes.POINTER(Options),
+         _ptr],
+    ),
+    "qr_geqrf_f32_route_codes_offset": (_size, [_int, _int]),
     "qr_fused_smalln_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr]),
     "qr_panel_f32": (
         _int,
@@ -69,7 +93,7 @@ SIGNATURES: dict[str, tuple] = {
 # qr_kernel_id values of include/qr_gfx950.h
 KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4, "apply": 5, "cholqr": 6}
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 QR_OK = 0
 
@@ -128,6 +152,13 @@ def trace_read(name: str) -> dict:
     check("qr_trace_read", load().qr_trace_read(KERNELS[name], ctypes.byref(cnt), ctypes.byref(ms),
                                                  ctypes.byref(fl), ctypes.byref(by)))
     return {"launches": cnt.value, "ms": ms.value, "flops": fl.value, "bytes": by.value}
+
+
+def default_options() -> Options:
+    """The options qr_geqrf_f32 runs with."""
+    o = Options()
+    load().qr_default_options(ctypes.byref(o))
+    return o
 
 
 def check(func: str, status: int) -> None:

@@ -86,8 +86,17 @@ def _residuals(A, H, tau, eye):
     return factor, orth, leak, recon
 
 
+def _worse(cur: float, new: float) -> float:
+    """The larger residual, NaN winning: Python's max(0.0, nan) is 0.0, which
+    would let a NaN factorisation pass."""
+    if cur != cur:
+        return cur
+    return new if (new != new or new > cur) else cur
+
+
 def check(A: torch.Tensor, H: torch.Tensor, tau: torch.Tensor) -> CheckResult:
-    """Validate a compact (H, tau) factorisation of A; residuals in FP64."""
+    """Validate a compact (H, tau) factorisation of A; residuals in FP64.
+    A NaN or Inf anywhere in (H, tau) gives a NaN or Inf residual and fails."""
     n = A.shape[-1]
     batch = A.shape[0]
     f_thr, o_thr = thresholds(n)
@@ -97,8 +106,8 @@ def check(A: torch.Tensor, H: torch.Tensor, tau: torch.Tensor) -> CheckResult:
     for s in range(0, batch, step):
         e = min(s + step, batch)
         f, o, lk, rc = _residuals(A[s:e], H[s:e], tau[s:e], eye)
-        factor, orth = max(factor, f), max(orth, o)
-        leak, recon = max(leak, lk), max(recon, rc)
+        factor, orth = _worse(factor, f), _worse(orth, o)
+        leak, recon = _worse(leak, lk), _worse(recon, rc)
     return CheckResult(
         n=n,
         batch=batch,

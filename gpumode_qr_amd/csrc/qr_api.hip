@@ -33,8 +33,10 @@ hipError_t launch_panel_seq(float* H, int64_t sHb, int64_t ldh, int J0, int nblk
 size_t cq_workspace_floats(int batch);
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
-                           int64_t sTwb, float* ws, int batch, hipStream_t stream);
+                           int64_t sTwb, float* ws, int batch, bool fused, bool one_pass,
+                           hipStream_t stream);
 const int* cq_flags(float* ws, int batch);
+size_t cq_flags_offset_floats(int batch);
 hipError_t launch_cq_reset(float* ws, int batch, hipStream_t stream);
 hipError_t launch_trail(float* H, int64_t sHb, int64_t ldh, int J0, int nblk, int r, int c0,
                         int ncols, const float* Tws, int64_t sTwb, const float* A, int64_t sAb,
@@ -56,7 +58,7 @@ hipError_t launch_eye(float* Q, int64_t sQb, int64_t ldq, int batch, int n, hipS
 
 namespace {
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 constexpr int kMaxN = 4096;
 constexpr int kSmallN = 64;
 constexpr int kPanel = 16;
@@ -77,27 +79,26 @@ size_t ws_cq_bytes(int batch) { return align_up(qr::cq_workspace_floats(batch) *
 // Outer blocks of 64 columns with at least this many rows take the CholeskyQR2
 // route: 128 rows in calls of at most 64 matrices, 512 above (with many
 // matrices the Householder panels of short blocks are throughput-bound and
-// cheaper). QR_CHOLQR=0 switches the route off; QR_CHOLQR_MIN_ROWS overrides
-// the bound (the route needs r > 64).
-int cq_min_rows(int batch) {
-  if (const char* env = std::getenv("QR_CHOLQR"))
-    if (env[0] == '0') return 1 << 30;
-  if (const char* env = std::getenv("QR_CHOLQR_MIN_ROWS")) {
-    const int v = std::atoi(env);
-    if (v >= 64) return v > 64 ? v : 65;
-  }
+// cheaper). opts->cholqr = 0 switches the route off; opts->cholqr_min_rows
+// sets the bound (the route needs r > 64).
+int cq_min_rows(int batch, const qr_options& o) {
+  if (!o.cholqr) return 1 << 30;
+  if (o.cholqr_min_rows) return o.cholqr_min_rows;
   return batch <= 64 ? 128 : 512;
 }
 
-// Panels per outer block for size n (QR_OUTER_BLOCKS=1..8 overrides).
-int outer_blocks(int n) {
-  if (const char* env = std::getenv("QR_OUTER_BLOCKS")) {
-    const int v = std::atoi(env);
-    if (v >= 1 && v <= kMaxBlocks) return v;
-  }
-  (void)n;
-  return 4;
+// Panels per outer block (opts->outer_panels, 0 = 4).
+int outer_blocks(const qr_options& o) { return o.outer_panels ? o.outer_panels : 4; }
+
+bool options_valid(const qr_options& o) {
+  return (o.cholqr == 0 || o.cholqr == 1) &&
+         (o.cholqr_min_rows == 0 || (o.cholqr_min_rows >= 65 && o.cholqr_min_rows <= kMaxN)) &&
+         (o.cholqr_one_pass == 0 || o.cholqr_one_pass == 1) &&
+         (o.cholqr_fused == 0 || o.cholqr_fused == 1) && (o.lookahead == 0 || o.lookahead == 1) &&
+         o.outer_panels >= 0 && o.outer_panels <= kMaxBlocks;
 }
+
+constexpr qr_options kDefaultOptions = {1, 0, 1, 0, 1, 0};
 
 int to_status(hipError_t e) { return e == hipSuccess ? QR_OK : QR_ELAUNCH; }
 
@@ -217,11 +218,12 @@ hipError_t run_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, i
 // rows below times M); bytes: the block read three times, V written once.
 hipError_t run_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                         int64_t ldh, int r, float* tau, int64_t sTaub, float* T, int64_t sTb,
-                        float* ws, int batch, hipStream_t s) {
+                        float* ws, int batch, const qr_options& o, hipStream_t s) {
   const double flops = 4.0 * 2.0 * r * 64.0 * 64.0 * 0.625 * batch;
   const double bytes = 4.0 * r * 64.0 * 4.0 * batch;
   return traced(QR_KERNEL_CHOLQR, flops, bytes, s, [&] {
-    return qr::launch_cq_block(Src, sSb, lds, Hb, sHb, ldh, r, tau, sTaub, T, sTb, ws, batch, s);
+    return qr::launch_cq_block(Src, sSb, lds, Hb, sHb, ldh, r, tau, sTaub, T, sTb, ws, batch,
+                               o.cholqr_fused != 0, o.cholqr_one_pass != 0, s);
   });
 }
 
@@ -292,12 +294,6 @@ bool lookahead_for_current_device(Lookahead* out) {
   return true;
 }
 
-// Look-ahead on/off (QR_LOOKAHEAD=0 disables it).
-bool lookahead_enabled() {
-  const char* env = std::getenv("QR_LOOKAHEAD");
-  return !(env && env[0] == '0');
-}
-
 }  // namespace
 
 extern "C" {
@@ -330,8 +326,26 @@ int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, f
   return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, static_cast<hipStream_t>(stream)));
 }
 
+void qr_default_options(qr_options* opts) {
+  if (opts) *opts = kDefaultOptions;
+}
+
+size_t qr_geqrf_f32_route_codes_offset(int batch, int n) {
+  if (batch <= 0 || n <= kSmallN || n > kMaxN) return 0;
+  return 2 * ws_t_bytes(batch) + qr::cq_flags_offset_floats(batch) * sizeof(float);
+}
+
 int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
                  int batch, int n, void* workspace, size_t workspace_bytes, void* stream) {
+  return qr_geqrf_f32_ex(A, sAb, sAr, sAc, H, tau, batch, n, workspace, workspace_bytes, nullptr,
+                         stream);
+}
+
+int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
+                    int batch, int n, void* workspace, size_t workspace_bytes,
+                    const qr_options* opts, void* stream) {
+  const qr_options o = opts ? *opts : kDefaultOptions;
+  if (!options_valid(o)) return QR_EINVAL;
   int st = check_geqrf_args(A, sAb, sAr, sAc, H, tau, batch, n);
   if (st != QR_OK || batch == 0 || n == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -345,7 +359,7 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   float* Tslot[2] = {static_cast<float*>(workspace),
                      static_cast<float*>(workspace) + (size_t)batch * kTStride};
   float* cq_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * ws_t_bytes(batch));
-  const int cq_rows = cq_min_rows(batch);
+  const int cq_rows = cq_min_rows(batch, o);
   bool cq_ready = false;
 
   // With a unit column stride the first outer block reads A itself: its panels
@@ -359,7 +373,7 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
     });
     if (e != hipSuccess) return QR_ELAUNCH;
   }
-  const int P = outer_blocks(n);
+  const int P = outer_blocks(o);
   const int NB = kPanel * P;
 
   // Look-ahead schedule. On the caller's stream s: the panels of block k, then
@@ -370,7 +384,7 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
   //   s waits for "rest of block k done" before touching columns >= J0 + 2 NB;
   //   at the end s waits for everything s2 did ("all done").
   Lookahead la;
-  const bool use_la = lookahead_enabled() && n > 2 * NB && lookahead_for_current_device(&la);
+  const bool use_la = o.lookahead && n > 2 * NB && lookahead_for_current_device(&la);
   std::unique_lock<std::mutex> la_lock(g_la_call_mu, std::defer_lock);
   if (use_la) la_lock.lock();
   bool rest_pending = false;  // s2 holds work that s must wait for
@@ -393,7 +407,7 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
       const float* Src = Ab ? Ab : H + (int64_t)J0 * n + J0;
       const int64_t sSb = Ab ? sAb : nn, lds = Ab ? sAr : n;
       e = run_cq_block(Src, sSb, lds, H + (int64_t)J0 * n + J0, nn, n, r, tau + J0, n, Tws,
-                       kTStride, cq_ws, batch, s);
+                       kTStride, cq_ws, batch, o, s);
       if (e != hipSuccess) return QR_ELAUNCH;
       only = qr::cq_flags(cq_ws, batch);
     }

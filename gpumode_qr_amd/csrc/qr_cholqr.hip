@@ -30,8 +30,6 @@
 // A matrix that fails any of them gets its flag set and none of its outputs
 // written; the panel launches that follow factor exactly those matrices by
 // Householder column steps and return at once for the others.
-#include <cstdlib>
-
 #include "qr_wy.hpp"
 
 namespace qr {
@@ -521,10 +519,14 @@ __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
           part + ((int64_t)b * nchunk + c) * kCqSlot + kCqPart);
     const bool ok = __all(piv[j] >= kCqPivMin && piv[j] <= 3.0e38f) && *dbad == 0 &&
                     nzm == ~0ull;
-    // One pass is enough when kappa(R1s) <= ||R1s||_F ||R1s^-1||_F = 8 ||R1s^-1||_F
-    // (unit columns) is at most 96: Q1 = A_b M1 is then orthonormal to about
-    // kappa^2 times the Gram's rounding (below 4e-5), as close as the second
-    // pass would make it for the (V, tau, R) it feeds.
+    // One pass is enough when ||R1s^-1||_F^2 <= 144. With unit columns
+    // sum(sigma_i^2) = ||R1s||_F^2 = 64, so sum(sigma_i^-2) <= 144 caps
+    // kappa_2(R1s) at 34.0 (sigma_max^2 = 22.7, sigma_min^2 = 1/51, the other
+    // 62 at 2/3). Q1 = A_b M1 is then orthonormal to about kappa^2 u, and the
+    // (V, tau, R) built from it differ from LAPACK sgeqrf's by at most 8e-6 at
+    // kappa = 37 and 4e-5 at kappa = 92 in a numpy model of these steps (r =
+    // 128; 2.7e-6 and 1.3e-5 at r = 1024), under the parity tolerance 4 r eps32
+    // (6.1e-5 at r = 128).
     const float ssum = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
     const bool single = allow_single && ssum <= kCqSingleMaxF2;
     if (j == 0) flags[b] = ok ? (single ? kCqFlagSingle : kCqFlagTwo) : kCqFlagFallback;
@@ -788,9 +790,9 @@ __global__ __launch_bounds__(64 * kCqGramWaves(kFused)) void k_cq_gram(const flo
 // after Gram kernels launched without kFused.
 __global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part, int nchunk,
                                                   float* __restrict__ mats, int64_t sMb,
-                                                  int* __restrict__ flags) {
+                                                  int* __restrict__ flags, int allow_single) {
   __shared__ __attribute__((aligned(16))) float smem[kCqChol1Lds + 8];
-  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, true);
+  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, allow_single != 0);
 }
 
 __global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part, int nchunk,
@@ -861,15 +863,8 @@ constexpr int kCqMaxChunks = 16;
 // save two launches per block but measured slower at every shape tried (b2
 // n4096 9.48 vs 9.19 ms, b16 n2048 7.07 vs 5.69 ms): the fused pass-2 kernel's
 // 137 KB of LDS per workgroup keeps its workgroups off the CUs that the
-// concurrent trailing update holds. Off by default; QR_CHOLQR_FUSED=1 selects
-// them (or calls of at most QR_CQ_FUSED_MAX_BATCH matrices at build time).
-#ifndef QR_CQ_FUSED_MAX_BATCH
-#define QR_CQ_FUSED_MAX_BATCH 0
-#endif
-bool cq_fused(int batch) {
-  if (const char* env = std::getenv("QR_CHOLQR_FUSED")) return env[0] == '1';
-  return batch <= QR_CQ_FUSED_MAX_BATCH;
-}
+// concurrent trailing update holds. The caller selects them (`fused`); the
+// default options do not.
 
 // Workspace floats of the CholeskyQR2 route for `batch` matrices: Gram
 // partials, three 64 x 64 matrices per matrix, flags.
@@ -880,13 +875,13 @@ size_t cq_workspace_floats(int batch) {
 }
 
 // The launches of one block: Gram 1, pass 1, Gram 2, pass 2 (each pair one
-// launch with cq_fused), then V. Src / Hb point at the block's top-left
+// launch when fused), then V. Src / Hb point at the block's top-left
 // element of matrix 0; ws holds cq_workspace_floats(batch) floats.
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
-                           int64_t sTwb, float* ws, int batch, hipStream_t stream) {
+                           int64_t sTwb, float* ws, int batch, bool fused, bool one_pass,
+                           hipStream_t stream) {
   if (r <= kCqB || r > kMaxStripRows || batch < 1) return hipErrorInvalidValue;
-  const bool fused = cq_fused(batch);
   const int gw = kCqGramWaves(fused);
   int rc = 0, nc = 0;
   cq_chunks(r, batch, kCqMaxChunks, 16 * gw, &rc, &nc);
@@ -909,7 +904,7 @@ hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb
                        r, rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws,
                        sTwb);
     hipLaunchKernelGGL(k_cq_chol1, dim3(batch), dim3(256), 0, stream, (const float*)part, nc,
-                       mats, sMb, flags);
+                       mats, sMb, flags, one_pass ? 1 : 0);
     hipLaunchKernelGGL((k_cq_gram<true, false>), dim3(g1), dim3(64 * gw), 0, stream, Src, sSb, lds, r,
                        rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
     hipLaunchKernelGGL(k_cq_recon, dim3(batch), dim3(256), 0, stream, (const float*)part, nc, mats,
@@ -943,12 +938,16 @@ hipError_t launch_cq_reset(float* ws, int batch, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Flags of the last launch_cq_block (for the fallback panels).
-const int* cq_flags(float* ws, int batch) {
+// Offset (floats) of the per-matrix flags in the route's workspace.
+size_t cq_flags_offset_floats(int batch) {
   int ncw = (256 + batch - 1) / batch;
   if (ncw > kCqMaxChunks) ncw = kCqMaxChunks;
-  return reinterpret_cast<const int*>(ws + (size_t)batch * ncw * kCqSlot +
-                                      (size_t)batch * 3 * kCqMat);
+  return (size_t)batch * ncw * kCqSlot + (size_t)batch * 3 * kCqMat;
+}
+
+// Flags of the last launch_cq_block (for the fallback panels).
+const int* cq_flags(float* ws, int batch) {
+  return reinterpret_cast<const int*>(ws + cq_flags_offset_floats(batch));
 }
 
 }  // namespace qr

@@ -1,8 +1,17 @@
-"""Results DB writer: one JSON file per run.
+"""Run records in the reference's results-DB form: one JSON file per run.
 
-Same record schema as the reference (src/qrbench/dbwrite.py:61-93): impl, git
-commit, date, ROCm version, docker image, torch version, GPU name,
-HIP_VISIBLE_DEVICES, ``benchmark_results`` (one entry per shape) and ``extra``.
+What is kept alike is the schema its readers depend on (reference
+src/qrbench/dbwrite.py:61-93, AGENTS.md): the file name
+``<UTC yyyymmddThhmmssZ>_<impl>.json`` and the top-level keys, in the order of
+``RECORD_KEYS``, with ``extra`` present only when given. How each provenance
+field is obtained is this module's own:
+
+* ``git_commit``: ``QR_SOURCE_REVISION`` if set (a copy of the tree without
+  its ``.git``, as on a remote GPU host, can be told its revision), else
+  ``git rev-parse HEAD`` with ``-dirty`` appended when tracked files differ
+  from it (``git status --porcelain --untracked-files=no``), else "unknown";
+* ``rocm_version``: the HIP version torch was built against;
+* ``gpu_name``: device 0 as torch names it ("cpu" without a GPU).
 """
 
 from __future__ import annotations
@@ -15,53 +24,57 @@ from pathlib import Path
 
 import torch
 
+RECORD_KEYS = ("impl", "git_commit", "date", "rocm_version", "docker_image", "torch_version",
+               "gpu_name", "hip_visible_devices", "benchmark_results", "extra")
 
-def _git_commit(repo_dir: str) -> str:
-    env_commit = os.environ.get("GIT_COMMIT")
-    if env_commit:
-        return env_commit
+
+def _git(repo_dir: str, *args: str) -> str | None:
     try:
-        out = subprocess.check_output(["git", "-C", repo_dir, "rev-parse", "HEAD"],
-                                      stderr=subprocess.DEVNULL)
-        dirty = subprocess.call(["git", "-C", repo_dir, "diff", "--quiet"],
-                                stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
-        return out.decode().strip() + ("-dirty" if dirty else "")
-    except Exception:
+        done = subprocess.run(["git", "-C", repo_dir, *args], capture_output=True, text=True,
+                              timeout=30)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    return done.stdout.strip() if done.returncode == 0 else None
+
+
+def source_revision(repo_dir: str) -> str:
+    given = os.environ.get("QR_SOURCE_REVISION")
+    if given:
+        return given
+    head = _git(repo_dir, "rev-parse", "HEAD")
+    if not head:
         return "unknown"
+    changes = _git(repo_dir, "status", "--porcelain", "--untracked-files=no")
+    return head + ("-dirty" if changes else "")
 
 
-def _rocm_version() -> str:
-    hip = getattr(torch.version, "hip", None)
-    if hip:
-        return hip
-    for p in ("/opt/rocm/.info/version", "/opt/rocm/.info/version-dev"):
-        try:
-            return Path(p).read_text().strip()
-        except OSError:
-            continue
-    return "unknown"
-
-
-def collect_metadata(repo_dir: str, docker_image: str | None = None) -> dict:
+def provenance(repo_dir: str, docker_image: str | None = None) -> dict:
+    """The record's provenance fields, in schema order."""
+    has_gpu = torch.cuda.is_available()
     return {
-        "git_commit": _git_commit(repo_dir),
+        "git_commit": source_revision(repo_dir),
         "date": datetime.now(timezone.utc).isoformat(),
-        "rocm_version": _rocm_version(),
-        "docker_image": docker_image or os.environ.get("DOCKER_IMAGE", "unknown"),
+        "rocm_version": getattr(torch.version, "hip", None) or "unknown",
+        "docker_image": docker_image or os.environ.get("DOCKER_IMAGE") or "unknown",
         "torch_version": torch.__version__,
-        "gpu_name": torch.cuda.get_device_name(0) if torch.cuda.is_available() else "cpu",
+        "gpu_name": torch.cuda.get_device_name(0) if has_gpu else "cpu",
         "hip_visible_devices": os.environ.get("HIP_VISIBLE_DEVICES", ""),
     }
 
 
-def write_result(db_dir: str, impl_name: str, metadata: dict, benchmark_results: list[dict],
-                 extra: dict | None = None) -> str:
-    Path(db_dir).mkdir(parents=True, exist_ok=True)
-    ts = datetime.now(timezone.utc).strftime("%Y%m%dT%H%M%SZ")
-    path = os.path.join(db_dir, f"{ts}_{impl_name}.json")
-    payload = {"impl": impl_name, **metadata, "benchmark_results": benchmark_results}
+def write_record(db_dir: str | Path, impl: str, provenance_fields: dict,
+                 benchmark_results: list[dict], extra: dict | None = None) -> Path:
+    """Write one record and return its path."""
+    fields = {"impl": impl, **provenance_fields, "benchmark_results": benchmark_results}
     if extra:
-        payload["extra"] = extra
-    with open(path, "w") as f:
-        json.dump(payload, f, indent=2)
+        fields["extra"] = extra
+    record = {k: fields[k] for k in RECORD_KEYS if k in fields}
+    missing = [k for k in RECORD_KEYS[:-1] if k not in record]
+    if missing:
+        raise KeyError(f"record lacks {missing}")
+    out = Path(db_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    stamp = datetime.now(timezone.utc).strftime("%Y%m%dT%H%M%SZ")
+    path = out / f"{stamp}_{impl}.json"
+    path.write_text(json.dumps(record, indent=2) + "\n")
     return path

@@ -13,6 +13,8 @@ the parity tests. Torch is only used for device memory and the stream.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -59,12 +61,26 @@ def workspace_bytes(batch: int, n: int) -> int:
     return int(_lib.load().qr_geqrf_f32_workspace(batch, n))
 
 
-def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None):
+def options(**changes) -> _lib.Options:
+    """Route options (``struct qr_options``): the defaults with ``changes``
+    applied, e.g. ``options(cholqr=0)`` or ``options(lookahead=0)``."""
+    o = _lib.default_options()
+    for name, value in changes.items():
+        if not hasattr(o, name):
+            raise TypeError(f"unknown route option {name!r}")
+        setattr(o, name, int(value))
+    return o
+
+
+def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None,
+          options: _lib.Options | None = None):
     """Batched compact-Householder QR on the GPU: ``(H, tau)`` like torch.geqrf.
 
-    The host work between the caller's stream position and the launch is kept
-    small (it is inside every event-timed call): no workspace query for n <= 64,
-    no device switch when ``A`` is on the current device.
+    ``options`` (from :func:`options`) selects a non-default route or
+    schedule; None runs the defaults. The host work between the caller's
+    stream position and the launch is kept small (it is inside every
+    event-timed call): no workspace query for n <= 64, no device switch when
+    ``A`` is on the current device.
     """
     _check_input(A)
     lib = _lib.load()
@@ -83,14 +99,29 @@ def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None):
     sb, sr, sc = A.stride()
     args = (A.data_ptr(), sb, sr, sc, H.data_ptr(), tau.data_ptr(), b, n, ws_ptr, ws_len)
     index = A.get_device()
+    if options is None:
+        call = lambda: lib.qr_geqrf_f32(*args, _stream_of(index))  # noqa: E731
+    else:
+        call = lambda: lib.qr_geqrf_f32_ex(*args, ctypes.byref(options),  # noqa: E731
+                                           _stream_of(index))
     if index == _current_device():
-        st = lib.qr_geqrf_f32(*args, _stream_of(index))
+        st = call()
     else:
         with torch.cuda.device(index):
-            st = lib.qr_geqrf_f32(*args, _stream_of(index))
+            st = call()
     if st:
         _lib.check("qr_geqrf_f32", st)
     return H, tau
+
+
+def route_codes(workspace: torch.Tensor, batch: int, n: int) -> torch.Tensor:
+    """Route of each matrix in the last 64-column block that took the
+    CholeskyQR2 route in the last geqrf call with this workspace:
+    0 two passes, 1 Householder panels (guard failed), 2 one pass."""
+    off = int(_lib.load().qr_geqrf_f32_route_codes_offset(batch, n))
+    if off == 0:
+        raise ValueError(f"no CholeskyQR2 workspace for batch={batch}, n={n}")
+    return workspace[off:off + 4 * batch].view(torch.int32).clone()
 
 
 def fused_smalln(A: torch.Tensor):

@@ -74,6 +74,50 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
                  int batch, int n, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Route and schedule choices of qr_geqrf_f32_ex. The library reads no
+ * environment variable: a call runs with exactly the options it is given
+ * (qr_geqrf_f32 uses qr_default_options). No counterpart in the reference,
+ * whose variants are separate registered functions (src/qrbench/variants.py:
+ * 920-1163); these select among the schedules of this one variant, for tests
+ * and measurements. Every choice gives the same (V, tau, R) within the parity
+ * tolerance; look-ahead and the panel count within an outer block give the
+ * same bits.
+ */
+typedef struct qr_options {
+  int cholqr;          /* 1 (default): 64-column outer blocks of >= cholqr_min_rows rows take
+                          the CholeskyQR2 route; 0: Householder panels for every block */
+  int cholqr_min_rows; /* 0 (default): 128 rows in calls of <= 64 matrices, 512 above;
+                          else the row bound itself (>= 65) */
+  int cholqr_one_pass; /* 1 (default): one CholeskyQR pass where ||R1s^-1||_F^2 <= 144;
+                          0: always two */
+  int cholqr_fused;    /* 0 (default): five launches per block; 1: Gram and per-matrix
+                          steps fused (the last workgroup of a matrix does its step) */
+  int lookahead;       /* 1 (default): rest of the trailing update on a second stream */
+  int outer_panels;    /* 16-wide panels per outer block, 1..8; 0 (default): 4. The
+                          CholeskyQR2 route needs 4. */
+} qr_options;
+
+/* Fills *opts with the defaults qr_geqrf_f32 runs with. */
+void qr_default_options(qr_options* opts);
+
+/*
+ * qr_geqrf_f32 with explicit route options (NULL: the defaults). Returns
+ * QR_EINVAL for an option outside its documented range.
+ */
+int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
+                    int batch, int n, void* workspace, size_t workspace_bytes,
+                    const qr_options* opts, void* stream);
+
+/*
+ * Byte offset, within a qr_geqrf_f32 workspace for (batch, n), of `batch`
+ * int32 route codes written by the last 64-column block that took the
+ * CholeskyQR2 route in a call: 0 two passes, 1 Householder panels (the
+ * matrix failed the route's guard), 2 one pass. Diagnostic only (tests read
+ * it to know which route a matrix took); no counterpart in the reference.
+ */
+size_t qr_geqrf_f32_route_codes_offset(int batch, int n);
+
+/*
  * Kernel (a): fused small-n factorisation, n <= 64, one wavefront per matrix.
  * Replaces hh_fused_qr / _hh_fused_qr_kernel (reference
  * src/qrbench/triton_kernels.py:641-755). Same arguments as qr_geqrf_f32.

@@ -1,8 +1,12 @@
 """Parity of the gfx950 HIP path against the CPU oracle, through the C ABI.
 
-Each test prints its case before touching the GPU so a failing run names it.
-Tolerance (tests/parity.py): |dV|, |dtau|, |dR|/||A[:,j]||_2 <= 4 n eps32 on
-well-conditioned inputs; rank-deficient and cond-1e6 inputs are gates-only.
+Each test prints its case before touching the GPU so a failing run names it,
+and every comparison prints its largest errors and tolerance ratio.
+Tolerance (tests/parity.py): |dV|, |dtau|, |dR|/||A[:,j]||_2 <= 4 n eps32 for
+n > 64 (plus fp32's subnormal floor from a subnormal column on); the
+cond-1e6 half of the stress config and near-duplicate columns are gates-only.
+Route and schedule choices are passed per call (hip_qr.options); the library
+reads no environment variable.
 """
 
 from __future__ import annotations
@@ -12,6 +16,7 @@ import pytest
 import torch
 
 from gpumode_qr_amd import checker, hip_qr, inputs
+from tests.blocks import near_bound_block
 from tests.parity import assert_parity
 
 pytestmark = pytest.mark.gpu
@@ -31,10 +36,20 @@ def _gauss(batch, n, seed, cond=0.0):
     return A
 
 
-def _run(A_cpu):
-    H, tau = hip_qr.geqrf(A_cpu.to(DEV))
+def _run(A_cpu, **opts):
+    H, tau = hip_qr.geqrf(A_cpu.to(DEV), options=hip_qr.options(**opts) if opts else None)
     torch.cuda.synchronize()
     return H.cpu(), tau.cpu()
+
+
+def _run_ws(A_cpu, **opts):
+    """geqrf with a workspace of our own, so the route codes can be read."""
+    b, n, _ = A_cpu.shape
+    ws = torch.empty(hip_qr.workspace_bytes(b, n), dtype=torch.uint8, device=DEV)
+    H, tau = hip_qr.geqrf(A_cpu.to(DEV), workspace=ws,
+                          options=hip_qr.options(**opts) if opts else None)
+    torch.cuda.synchronize()
+    return H.cpu(), tau.cpu(), hip_qr.route_codes(ws, b, n).cpu()
 
 
 @pytest.mark.parametrize("n", [1, 2, 3, 8, 17, 32, 33, 48, 63, 64])
@@ -276,7 +291,7 @@ def test_config1_parity_and_gates(oracle):
     H, tau = _run(A)
     assert checker.check(A, H, tau).passed
     H_ref, tau_ref = oracle.geqrf(A.numpy())
-    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="cfg1")
     Hm, tm = torch.geqrf(A)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), Hm.numpy(), tm.numpy(), what="vs MKL")
 
@@ -287,7 +302,7 @@ def test_config2_parity_and_gates(oracle):
     H, tau = _run(A)
     assert checker.check(A, H, tau).passed
     H_ref, tau_ref = oracle.geqrf(A.numpy())
-    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="cfg2 full batch")
 
 
 def test_config4_gates_and_sampled_parity(oracle):
@@ -295,9 +310,10 @@ def test_config4_gates_and_sampled_parity(oracle):
     A = inputs.config_tensor(inputs.config_spec(4))
     H, tau = _run(A)
     assert checker.check(A, H, tau).passed
-    idx = [0, 37]
+    idx = [0, 21, 37, 63]
     H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
-    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref)
+    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref,
+                  what="cfg4 sampled")
 
 
 def test_config5_gates_and_gaussian_half_parity(oracle):
@@ -309,17 +325,28 @@ def test_config5_gates_and_gaussian_half_parity(oracle):
     assert res.passed, res.as_dict()
     n = A.shape[-1]
     assert torch.all(tau[8:, n // 3] == 0)  # zeroed column -> identity reflector
-    idx = [8, 15]
+    idx = [8, 11, 15]
     H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
-    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref)
+    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref,
+                  what="cfg5 Gaussian half")
 
 
-def test_config3_gates_sampled():
-    _say("config 3 (b640 n512), first 64 matrices")
-    A = inputs.config_tensor(inputs.config_spec(3))[:64]
-    H, tau = _run(A)
+def test_config3_full_batch_gates_and_sampled_parity(oracle):
+    """All 640 matrices through the default route, as the benchmark runs them
+    (more than 64 matrices: the CholeskyQR2 route on the first, 512-row block
+    only, then the 4-wave panels and the b640 trailing-update shapes). Gates on
+    the whole batch, oracle parity on five matrices spread over it."""
+    _say("config 3 (b640 n512), full batch")
+    A = inputs.config_tensor(inputs.config_spec(3))
+    H, tau, codes = _run_ws(A)
+    assert torch.isfinite(H).all() and torch.isfinite(tau).all()
     res = checker.check(A, H, tau)
     assert res.passed, res.as_dict()
+    assert bool((codes != 1).all())  # no matrix left the route in its block
+    idx = [0, 157, 320, 481, 639]
+    H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
+    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref,
+                  what="cfg3 sampled")
 
 
 def test_input_not_modified_and_repeatable():
@@ -414,12 +441,12 @@ def test_concurrent_host_threads_bitwise():
 
 @pytest.mark.parametrize("lookahead", ["1", "0"])
 @pytest.mark.parametrize("n", [100, 700, 1100])
-def test_first_block_reads_padded_input_directly(monkeypatch, n, lookahead):
+def test_first_block_reads_padded_input_directly(n, lookahead):
     """Input with a unit column stride but padded rows and batch (row stride
     n + 7, batch stride (n + 3) (n + 7)) is read in place by the first outer
     block's kernels; a column-major view of the same values goes through the
     strided copy first. Both give the same bits, with and without look-ahead."""
-    monkeypatch.setenv("QR_LOOKAHEAD", lookahead)
+    opts = hip_qr.options(lookahead=int(lookahead))
     _say(f"padded input read directly (n={n}, lookahead={lookahead})")
     batch = 2
     base = torch.randn(batch, n + 3, n + 7, generator=torch.Generator().manual_seed(n))
@@ -427,8 +454,8 @@ def test_first_block_reads_padded_input_directly(monkeypatch, n, lookahead):
     assert Ap.stride() == ((n + 3) * (n + 7), n + 7, 1)
     Ac = Ap.transpose(1, 2).contiguous().transpose(1, 2)
     assert Ac.stride(2) == n and torch.equal(Ac, Ap)
-    Hp, tp = hip_qr.geqrf(Ap)
-    Hc, tc = hip_qr.geqrf(Ac)
+    Hp, tp = hip_qr.geqrf(Ap, options=opts)
+    Hc, tc = hip_qr.geqrf(Ac, options=opts)
     torch.cuda.synchronize()
     assert torch.equal(Hp, Hc) and torch.equal(tp, tc)
     assert torch.equal(Ap, Ac)  # the input is left as it was
@@ -438,26 +465,23 @@ def test_first_block_reads_padded_input_directly(monkeypatch, n, lookahead):
 # their update over two streams, the late ones fit in one round and run as one
 # launch; (300, 3) and (1100, 2) fit in one round from early on.
 @pytest.mark.parametrize("n,batch", [(300, 3), (1100, 2), (700, 64)])
-def test_lookahead_schedule_is_bitwise_identical(monkeypatch, n, batch):
+def test_lookahead_schedule_is_bitwise_identical(n, batch):
     # The look-ahead schedule only splits the trailing update into disjoint
     # column ranges on two streams: results must not change by a single bit.
     _say(f"look-ahead on/off n={n}")
     A = _gauss(batch, n, seed=n + 1).to(DEV)
-    monkeypatch.setenv("QR_LOOKAHEAD", "0")
-    H0, t0 = hip_qr.geqrf(A)
+    H0, t0 = hip_qr.geqrf(A, options=hip_qr.options(lookahead=0))
     torch.cuda.synchronize()
-    monkeypatch.setenv("QR_LOOKAHEAD", "1")
-    H1, t1 = hip_qr.geqrf(A)
+    H1, t1 = hip_qr.geqrf(A, options=hip_qr.options(lookahead=1))
     torch.cuda.synchronize()
     assert torch.equal(H0, H1) and torch.equal(t0, t1)
 
 
 @pytest.mark.parametrize("P", [1, 2, 3, 8])
-def test_outer_block_widths(monkeypatch, oracle, P):
+def test_outer_block_widths(oracle, P):
     _say(f"outer block of {P} panels, n=400")
-    monkeypatch.setenv("QR_OUTER_BLOCKS", str(P))
     A = _gauss(2, 400, seed=P)
-    H, tau = _run(A)
+    H, tau = _run(A, outer_panels=P)
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"P={P}")
 
@@ -579,31 +603,99 @@ def test_run_baseline_db_record_schema(tmp_path):
 
 # --------------------------------------------------------------------------
 # Outer blocks by CholeskyQR2 + Householder reconstruction (qr_cholqr.hip).
-# QR_CHOLQR_MIN_ROWS=64 sends every full 64-column block through the route
-# (by default only blocks of >= 256 rows take it); QR_CHOLQR=0 switches it off.
+# cholqr_min_rows=65 sends every full 64-column block through the route (by
+# default blocks of >= 128 rows in calls of <= 64 matrices, >= 512 above);
+# cholqr=0 switches it off. Route codes of the last route block: 0 two
+# passes, 1 Householder panels (guard failed), 2 one pass.
+
+EVERY_BLOCK = {"cholqr_min_rows": 65}
+
 
 @pytest.mark.parametrize("n", [128, 129, 200, 256, 300, 513, 1100])
-def test_cholqr_route_vs_oracle(monkeypatch, oracle, n):
+def test_cholqr_route_vs_oracle(oracle, n):
     _say(f"cholqr route (every full block) n={n}")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
     A = _gauss(3, n, seed=n + 11)
-    H, tau = _run(A)
+    H, tau = _run(A, **EVERY_BLOCK)
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"cholqr n={n}")
     res = checker.check(A, H, tau)
     assert res.passed, res.as_dict()
 
 
-def test_cholqr_route_cond1e2_svd(monkeypatch, oracle):
+def test_cholqr_route_cond1e2_svd(oracle):
+    """Haar-SVD input of cond 1e2, every block on the route; then the first
+    block alone (cholqr_min_rows = n): its ||R1s^-1||_F^2 > 144, so it takes
+    two passes. The route codes are those of the last route block."""
     _say("cholqr route, cond-1e2 SVD input b2 n512")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
-    A = inputs.svd_matrices(2, 512, 2.0, torch.Generator().manual_seed(5))
-    A = A.float()
-    H, tau = _run(A)
+    A = inputs.svd_matrices(2, 512, 2.0, torch.Generator().manual_seed(5)).float()
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    H, tau = _run(A, **EVERY_BLOCK)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="cholqr svd")
     res = checker.check(A, H, tau)
     assert res.passed, res.as_dict()
+    H, tau, codes = _run_ws(A, cholqr_min_rows=512)
+    assert codes.tolist() == [0, 0], codes
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="svd first block")
+
+
+@pytest.mark.parametrize("shape", [(60, 1024), (8, 2048), (2, 4096)],
+                         ids=["b60_n1024", "b8_n2048", "b2_n4096"])
+def test_cholqr_default_route_official_shapes_vs_oracle(oracle, shape):
+    """The shapes where the route factors most of V, tau and R by default
+    (every block of >= 128 rows): the official inputs (columns scaled by
+    logspace(0, -cond, n)), gates on the batch and oracle parity on one
+    matrix. The route codes show the last route block's path."""
+    batch, n = shape
+    spec = next(s for s in inputs.BENCHMARK_SHAPES if (s["batch"], s["n"]) == shape)
+    _say(f"cholqr default route, official shape b{batch} n{n}")
+    A = inputs.make_benchmark_problem(spec, seed=7, device="cpu").tensor
+    H, tau, codes = _run_ws(A)
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+    assert bool((codes != 1).all()), codes
+    H_ref, tau_ref = oracle.geqrf(A[:1].numpy(), nb=16)
+    assert_parity(A[:1].numpy(), H[:1].numpy(), tau[:1].numpy(), H_ref, tau_ref,
+                  what=f"b{batch} n{n} matrix 0")
+
+
+@pytest.mark.parametrize("inv_sum,code", [(140.0, 2), (152.0, 0)], ids=["one_pass", "two_pass"])
+def test_cholqr_one_pass_bound_vs_oracle(oracle, inv_sum, code):
+    """First block of n = 160 (the only route block of the call) at the
+    one-pass bound: sum(sigma^-2) of the scaled Gram just under 144 takes one
+    pass at kappa about 33, just over it takes two. Both match the oracle at
+    the flat tolerance."""
+    n = 160
+    _say(f"cholqr one-pass bound n={n} sum(1/sigma^2)={inv_sum}")
+    g = torch.Generator().manual_seed(41)
+    A = torch.randn(2, n, n, generator=g)
+    for b in range(2):
+        blk, kappa = near_bound_block(n, inv_sum, seed=b)
+        A[b, :, :64] = torch.from_numpy(blk)
+    H, tau, codes = _run_ws(A)
+    print(f"[gpu-case] near-bound kappa(R1s) about {kappa:.1f}, codes {codes.tolist()}",
+          flush=True)
+    assert codes.tolist() == [code, code], codes
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref,
+                  what=f"one-pass bound code {code}")
+
+
+@pytest.mark.parametrize("n", [300, 2048])
+def test_cholqr_forced_two_passes_vs_oracle(oracle, n):
+    """The first block of a Gaussian matrix (the only route block with
+    cholqr_min_rows = n) takes one pass by default; cholqr_one_pass=0 forces
+    the second pass for the same input."""
+    _say(f"cholqr forced two passes n={n}")
+    A = _gauss(2, n, seed=n + 21)
+    H1, t1, c1 = _run_ws(A, cholqr_min_rows=n)
+    H2, t2, c2 = _run_ws(A, cholqr_one_pass=0, cholqr_min_rows=n)
+    assert c1.tolist() == [2, 2] and c2.tolist() == [0, 0], (c1, c2)
+    assert not torch.equal(H1, H2)  # the two paths round differently
+    idx = [0] if n > 1024 else [0, 1]
+    H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
+    for H, tau, what in ((H1, t1, "one pass"), (H2, t2, "two passes")):
+        assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref,
+                      what=f"n={n} {what}")
 
 
 # A block whose Gram is singular, out of range, or too ill-conditioned for
@@ -611,9 +703,8 @@ def test_cholqr_route_cond1e2_svd(monkeypatch, oracle):
 # other matrices of the batch keep the route in the same block.
 @pytest.mark.parametrize("n,cols", [(300, (20, 150, 290)), (700, (5, 400, 650))])
 @pytest.mark.parametrize("kind", ["zero", "tiny", "huge", "denormal", "near_dup"])
-def test_cholqr_fallback_vs_oracle(monkeypatch, oracle, n, cols, kind):
+def test_cholqr_fallback_vs_oracle(oracle, n, cols, kind):
     _say(f"cholqr fallback {kind} n={n} cols={cols}")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
     A = _gauss(3, n, seed=n + 3)
     for b, c in ((0, cols[0]), (1, cols[1]), (1, cols[2])):
         if kind == "zero":
@@ -622,7 +713,7 @@ def test_cholqr_fallback_vs_oracle(monkeypatch, oracle, n, cols, kind):
             A[b, :, c + 1 if c + 1 < n else c - 1] = A[b, :, c] * (1 + 1e-6)
         else:
             A[b, :, c] *= {"tiny": 1e-30, "huge": 1e25, "denormal": 1e-40}[kind]
-    H, tau = _run(A)
+    H, tau = _run(A, **EVERY_BLOCK)
     assert torch.isfinite(H).all() and torch.isfinite(tau).all()
     if kind != "near_dup":  # near-duplicate columns: kappa ~1e7, gates only
         H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
@@ -633,42 +724,52 @@ def test_cholqr_fallback_vs_oracle(monkeypatch, oracle, n, cols, kind):
         assert res.passed, res.as_dict()
 
 
+@pytest.mark.parametrize("kind", ["zero", "tiny", "denormal"])
+def test_cholqr_fallback_route_codes(kind):
+    """n = 160 with only the first block on the route: a zero, tiny (1e-30
+    outside the Gram's [1e-30, 1e30] diagonal range once squared) or
+    subnormal column in it sends that matrix, and only it, to the panels."""
+    n = 160
+    _say(f"cholqr fallback route code {kind} n={n}")
+    A = _gauss(3, n, seed=77)
+    A[1, :, 30] = 0.0 if kind == "zero" else A[1, :, 30] * (1e-30 if kind == "tiny" else 1e-40)
+    _, _, codes = _run_ws(A)
+    assert codes.tolist() == [2, 1, 2], codes
+
+
 @pytest.mark.parametrize("n,batch", [(300, 3), (1100, 2), (700, 64)])
-def test_cholqr_lookahead_and_repeat_bitwise(monkeypatch, n, batch):
+def test_cholqr_lookahead_and_repeat_bitwise(n, batch):
     _say(f"cholqr route look-ahead on/off and repeat n={n} b={batch}")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
     A = _gauss(batch, n, seed=n + 5).to(DEV)
-    monkeypatch.setenv("QR_LOOKAHEAD", "0")
-    H0, t0 = hip_qr.geqrf(A)
+    off = hip_qr.options(lookahead=0, **EVERY_BLOCK)
+    on = hip_qr.options(lookahead=1, **EVERY_BLOCK)
+    H0, t0 = hip_qr.geqrf(A, options=off)
     torch.cuda.synchronize()
-    monkeypatch.setenv("QR_LOOKAHEAD", "1")
-    H1, t1 = hip_qr.geqrf(A)
-    H2, t2 = hip_qr.geqrf(A)
+    H1, t1 = hip_qr.geqrf(A, options=on)
+    H2, t2 = hip_qr.geqrf(A, options=on)
     torch.cuda.synchronize()
     assert torch.equal(H0, H1) and torch.equal(t0, t1)
     assert torch.equal(H1, H2) and torch.equal(t1, t2)
 
 
-def test_cholqr_off_matches_on_within_tolerance(monkeypatch, oracle):
+def test_cholqr_off_matches_on_within_tolerance(oracle):
     _say("cholqr on vs off, b4 n600")
     A = _gauss(4, 600, seed=77)
-    monkeypatch.setenv("QR_CHOLQR", "0")
-    Hh, th = _run(A)
-    monkeypatch.delenv("QR_CHOLQR")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
-    Hc, tc = _run(A)
+    Hh, th = _run(A, cholqr=0)
+    Hc, tc = _run(A, **EVERY_BLOCK)
     assert not torch.equal(Hh, Hc)  # the two routes round differently
     assert_parity(A.numpy(), Hc.numpy(), tc.numpy(), Hh.numpy().astype(np.float64),
                   th.numpy().astype(np.float64), what="cholqr vs householder")
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), Hh.numpy(), th.numpy(), H_ref, tau_ref, what="householder only")
 
 
 @pytest.mark.parametrize("kind", ["upper", "block_diag"])
-def test_cholqr_exact_zero_structure(monkeypatch, oracle, kind):
+def test_cholqr_exact_zero_structure(oracle, kind):
     """Exact zeros below a diagonal give slarfg's tau = 0: upper-triangular input
     stays a fixed point (H == A, tau == 0) and a block-diagonal matrix matches
     the oracle, because such blocks leave the CholeskyQR2 route."""
     _say(f"cholqr route, exact-zero structure {kind} n=300")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "65")
     A = _gauss(2, 300, seed=9)
     if kind == "upper":
         A = torch.triu(A)
@@ -678,7 +779,7 @@ def test_cholqr_exact_zero_structure(monkeypatch, oracle, kind):
         for s0 in range(0, 300, 100):
             mask[s0:s0 + 100, s0:s0 + 100] = True
         A = torch.where(mask, A, torch.zeros(()))
-    H, tau = _run(A)
+    H, tau = _run(A, **EVERY_BLOCK)
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"cholqr {kind}")
     if kind == "upper":
@@ -687,28 +788,37 @@ def test_cholqr_exact_zero_structure(monkeypatch, oracle, kind):
 
 
 @pytest.mark.parametrize("n,batch", [(300, 3), (700, 5)])
-def test_cholqr_fused_variant(monkeypatch, oracle, n, batch):
-    """The fused Gram + per-matrix kernels (QR_CHOLQR_FUSED=1: the last
+def test_cholqr_fused_variant(oracle, n, batch):
+    """The fused Gram + per-matrix kernels (cholqr_fused=1: the last
     workgroup of a matrix to finish runs its per-matrix step, whichever it is)
     match the oracle, and each variant is bit-identical with look-ahead on and
     off. The two variants split the Gram rows over different wave counts, so
     they round differently from each other."""
     _say(f"cholqr fused and separate kernels n={n} b={batch}")
-    monkeypatch.setenv("QR_CHOLQR_MIN_ROWS", "64")
     A = _gauss(batch, n, seed=n + 9)
     A[1, :, 100] = 0.0  # one matrix takes the fallback panels in one block
     Ad = A.to(DEV)
     out = {}
-    for fused in ("0", "1"):
-        for la in ("0", "1"):
-            monkeypatch.setenv("QR_CHOLQR_FUSED", fused)
-            monkeypatch.setenv("QR_LOOKAHEAD", la)
-            out[fused, la] = hip_qr.geqrf(Ad)
+    for fused in (0, 1):
+        for la in (0, 1):
+            opts = hip_qr.options(cholqr_fused=fused, lookahead=la, **EVERY_BLOCK)
+            out[fused, la] = hip_qr.geqrf(Ad, options=opts)
     torch.cuda.synchronize()
-    for fused in ("0", "1"):
-        (H0, t0), (H1, t1) = out[fused, "0"], out[fused, "1"]
+    for fused in (0, 1):
+        (H0, t0), (H1, t1) = out[fused, 0], out[fused, 1]
         assert torch.equal(H0, H1) and torch.equal(t0, t1), fused
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
-    H, tau = out["1", "1"]
-    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
-                  what=f"fused n={n}")
+    for fused in (0, 1):
+        H, tau = out[fused, 1]
+        assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
+                      what=f"fused={fused} n={n}")
+
+
+def test_options_out_of_range_are_rejected():
+    _say("route options validation")
+    A = _gauss(1, 100, seed=1).to(DEV)
+    for bad in ({"cholqr": 2}, {"cholqr_min_rows": 64}, {"outer_panels": 9},
+                {"lookahead": -1}, {"cholqr_one_pass": 3}):
+        with pytest.raises(Exception) as ei:
+            hip_qr.geqrf(A, options=hip_qr.options(**bad))
+        assert getattr(ei.value, "status", None) == 1, bad

@@ -122,3 +122,29 @@ def test_hip_path_refuses_cpu_tensors():
         hip_qr.geqrf(torch.zeros(2, 8, 8))
     with pytest.raises(TypeError):
         hip_qr.geqrf(torch.zeros(2, 8, 8, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("chunk", [None, 1, 2])
+@pytest.mark.parametrize("kind", ["nan_in_v", "all_nan", "inf_in_tau", "nan_in_r"])
+def test_checker_fails_on_nan_and_inf(monkeypatch, chunk, kind):
+    # A factorisation holding NaN or Inf must fail the gates, whichever chunk
+    # of the batch it sits in (Python's max(0.0, nan) is 0.0).
+    g = torch.Generator().manual_seed(2)
+    A = torch.randn(5, 10, 10, generator=g)
+    H, tau = torch.geqrf(A)
+    if chunk is not None:
+        monkeypatch.setattr(checker, "_chunk", lambda b, n: chunk)
+    assert checker.check(A, H, tau).passed
+    H, tau = H.clone(), tau.clone()
+    if kind == "nan_in_v":
+        H[3, 7, 2] = float("nan")
+    elif kind == "all_nan":
+        H.fill_(float("nan"))
+        tau.fill_(float("nan"))
+    elif kind == "inf_in_tau":
+        tau[1, 4] = float("inf")
+    else:
+        H[0, 1, 5] = float("nan")
+    res = checker.check(A, H, tau)
+    assert not res.passed, res.as_dict()
+    assert not res.factor_pass or not res.orth_pass

@@ -21,7 +21,7 @@ def _declared_functions() -> set[str]:
     names = set()
     for hdr in INCLUDE.glob("*.h"):
         text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
-        for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(qr_\w+)\s*\(", text):
+        for m in re.finditer(r"\b(?:int|size_t|void|const char\*)\s+(qr_\w+)\s*\(", text):
             names.add(m.group(1))
     return names
 
@@ -99,3 +99,31 @@ def test_argument_validation_without_launch(lib):
     assert lib.qr_ormqr_f32(h, 0, 0, t, 0, p, 0, 0, 0, 8, 1, 1, None, 0, None) == 0  # n = 0
     assert lib.qr_orgqr_f32(h, 10000, 100, t, 100, h, 10000, 100, 100, 1, h, 1 << 20,
                             None) == 1  # Q overlaps H
+
+
+def test_route_options_defaults_and_validation(lib):
+    o = _lib.default_options()
+    assert o.as_dict() == {"cholqr": 1, "cholqr_min_rows": 0, "cholqr_one_pass": 1,
+                           "cholqr_fused": 0, "lookahead": 1, "outer_panels": 0}
+    p = ctypes.c_void_p(0x1000)
+    h = ctypes.c_void_p(0x10000000)
+    t = ctypes.c_void_p(0x20000000)
+    ex = lib.qr_geqrf_f32_ex
+    assert ex(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, None, None) == 3  # NULL: defaults
+    for field, bad in (("cholqr", 2), ("cholqr_min_rows", 64), ("cholqr_min_rows", 5000),
+                       ("cholqr_one_pass", -1), ("cholqr_fused", 2), ("lookahead", 7),
+                       ("outer_panels", 9), ("outer_panels", -1)):
+        o = _lib.default_options()
+        setattr(o, field, bad)
+        assert ex(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, ctypes.byref(o), None) == 1, field
+    o = _lib.default_options()
+    o.cholqr_min_rows = 65
+    assert ex(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, ctypes.byref(o), None) == 3
+
+
+def test_route_codes_lie_inside_the_workspace(lib):
+    for batch, n in ((1, 65), (2, 4096), (64, 1024), (640, 512), (2048, 128)):
+        off = lib.qr_geqrf_f32_route_codes_offset(batch, n)
+        assert 0 < off and off + 4 * batch <= lib.qr_geqrf_f32_workspace(batch, n)
+        assert off % 4 == 0
+    assert lib.qr_geqrf_f32_route_codes_offset(8, 64) == 0  # fused small-n route: none
