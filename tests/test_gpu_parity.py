@@ -623,19 +623,17 @@ def test_cholqr_route_vs_oracle(oracle, n):
 
 
 def test_cholqr_route_cond1e2_svd(oracle):
-    """Haar-SVD input of cond 1e2, every block on the route; then the first
-    block alone (cholqr_min_rows = n): its ||R1s^-1||_F^2 > 144, so it takes
-    two passes. The route codes are those of the last route block."""
+    """Haar-SVD input of cond 1e2 with every block on the route. (Its first
+    64 columns are well conditioned: 64 random combinations of 512 singular
+    directions. The two-pass path is pinned by the near-bound and forced
+    two-pass tests.)"""
     _say("cholqr route, cond-1e2 SVD input b2 n512")
     A = inputs.svd_matrices(2, 512, 2.0, torch.Generator().manual_seed(5)).float()
-    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     H, tau = _run(A, **EVERY_BLOCK)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="cholqr svd")
     res = checker.check(A, H, tau)
     assert res.passed, res.as_dict()
-    H, tau, codes = _run_ws(A, cholqr_min_rows=512)
-    assert codes.tolist() == [0, 0], codes
-    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="svd first block")
 
 
 @pytest.mark.parametrize("shape", [(60, 1024), (8, 2048), (2, 4096)],
