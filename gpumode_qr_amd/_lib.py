@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
          _ptr],
     ),
     "qr_geqrf_f32_route_codes_offset": (_size, [_int, _int]),
+    "qr_geqrf_f32_noalloc": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr]),
     "qr_fused_smalln_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _int, _int, _ptr]),
     "qr_panel_f32": (
         _int,

@@ -116,6 +116,9 @@ struct TraceRec {
 
 std::mutex g_trace_mu;
 unsigned g_trace_mask = 0;
+// Set while this thread runs qr_geqrf_f32_noalloc: its launches are never
+// traced, so it creates no events.
+thread_local bool t_untraced = false;
 std::vector<TraceRec> g_trace;
 std::vector<hipEvent_t> g_event_pool;
 
@@ -138,7 +141,7 @@ hipError_t traced(int kernel, double flops, double bytes, hipStream_t s, F&& lau
     std::lock_guard<std::mutex> lk(g_trace_mu);
     mask = g_trace_mask;
   }
-  if (!(mask & (1u << kernel))) return launch();
+  if (t_untraced || !(mask & (1u << kernel))) return launch();
   hipEvent_t a, b;
   {
     std::lock_guard<std::mutex> lk(g_trace_mu);
@@ -476,6 +479,59 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
       return QR_ELAUNCH;
   }
   return QR_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Workspace of qr_geqrf_f32_noalloc: a static device array, one copy on each
+// GPU the library runs on, held until the process ends. Host code must use
+// the per-device address from hipGetSymbolAddress, never `scratch` itself
+// (in host code that name is a host-side stand-in, not a device address).
+__device__ __align__(256) unsigned char scratch[QR_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current); nullptr if the lookup fails.
+void* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int qr_geqrf_f32_noalloc(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                         float* tau, int batch, int n, void* stream) {
+  int st = check_geqrf_args(A, sAb, sAr, sAc, H, tau, batch, n);
+  if (st != QR_OK || batch == 0 || n == 0) return st;
+  const size_t need = qr_geqrf_f32_workspace(batch, n);
+  if (need > QR_NOALLOC_SCRATCH_BYTES) return QR_EWORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_for_current_device();
+    if (!ws) return QR_ELAUNCH;
+  }
+  // Everything on the caller's stream: no second stream, no events, no
+  // occupancy query; the same kernels and results as with look-ahead.
+  qr_options o = kDefaultOptions;
+  o.lookahead = 0;
+  t_untraced = true;
+  st = qr_geqrf_f32_ex(A, sAb, sAr, sAc, H, tau, batch, n, ws, need, &o, stream);
+  t_untraced = false;
+  return st;
 }
 
 int qr_panel_f32(float* H, int64_t sHb, int64_t ldh, int j0, int p, int r, int kw, float* tau,

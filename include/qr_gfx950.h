@@ -117,6 +117,26 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
  */
 size_t qr_geqrf_f32_route_codes_offset(int batch, int n);
 
+/* Size of the static device workspace of qr_geqrf_f32_noalloc (per GPU). */
+#define QR_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * qr_geqrf_f32 for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference. The workspace is a static device array of
+ * QR_NOALLOC_SCRATCH_BYTES (64 MiB) that each GPU the library runs on holds
+ * until the process ends; the call allocates nothing, creates no stream or
+ * event, and enqueues every kernel on `stream` (no look-ahead stream), with
+ * results bit-identical to qr_geqrf_f32's. Returns QR_EWORKSPACE when
+ * qr_geqrf_f32_workspace(batch, n) exceeds the array (about 880 matrices of
+ * n = 512, 110 of n = 1024 up to 64). Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (two streams, two host threads)
+ * race, and must be ordered by the caller. The first call on a device looks
+ * up the array's device address (hipGetSymbolAddress).
+ */
+int qr_geqrf_f32_noalloc(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                         float* tau, int batch, int n, void* stream);
+
 /*
  * Kernel (a): fused small-n factorisation, n <= 64, one wavefront per matrix.
  * Replaces hh_fused_qr / _hh_fused_qr_kernel (reference
