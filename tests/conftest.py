@@ -35,3 +35,17 @@ def oracle():
 
     O.build()
     return O
+
+
+def pytest_terminal_summary(terminalreporter):
+    """One line per elementwise parity comparison that passed: the largest
+    |dV|, |dtau|, |dR|/||a_j|| and the worst error-to-tolerance ratio."""
+    from tests import parity
+
+    if not parity.MARGINS:
+        return
+    terminalreporter.section(f"parity margins ({len(parity.MARGINS)} comparisons)")
+    for line in parity.MARGINS:
+        terminalreporter.write_line(line)
+    worst = max(float(line.rsplit("=", 1)[1]) for line in parity.MARGINS)
+    terminalreporter.write_line(f"largest error/tolerance over all comparisons: {worst:.3f}")

@@ -50,6 +50,12 @@ EPS32 = 2.0**-23
 ETA32 = 2.0**-149  # spacing of the fp32 subnormals
 S0 = 10.0  # sensitivity at which the tolerance starts to widen
 
+# The one-line margin of every comparison that passed, in order;
+# tests/conftest.py prints them in pytest's terminal summary so a quiet (-q)
+# run still shows each margin. (A rejected comparison raises with its own
+# message instead.)
+MARGINS: list[str] = []
+
 
 def tolerance(n: int, c: float = 4.0) -> float:
     """The flat bound c n eps32."""
@@ -129,10 +135,11 @@ def assert_parity(A, H, tau, H_ref, tau_ref, tol: float | None = None, what: str
     worst = {"R": rR.max(initial=0.0), "V": rV.max(initial=0.0), "tau": rT.max(initial=0.0)}
     ratio = float(max(worst.values()))
     out = {**errs, "tol": tolerance(n) if tol is None else tol, "ratio": ratio}
+    line = (f"{what or 'case'}: n={n} batch={A.shape[0]} max|dV|={errs['V']:.2e} "
+            f"max|dtau|={errs['tau']:.2e} max|dR|/|a_j|={errs['R']:.2e} "
+            f"flat tol={out['tol']:.2e} worst/tol={ratio:.3f}")
     if not quiet:
-        print(f"[parity] {what or 'case'}: n={n} batch={A.shape[0]} max|dV|={errs['V']:.2e} "
-              f"max|dtau|={errs['tau']:.2e} max|dR|/|a_j|={errs['R']:.2e} "
-              f"flat tol={out['tol']:.2e} worst/tol={ratio:.3f}", flush=True)
+        print(f"[parity] {line}", flush=True)
     if not ratio <= 1.0:
         part = max(worst, key=lambda k: worst[k])
         arr = {"R": rR, "V": rV, "tau": rT}[part]
@@ -141,4 +148,5 @@ def assert_parity(A, H, tau, H_ref, tau_ref, tol: float | None = None, what: str
             f"{what}: parity beyond tolerance in {part} at (matrix, ...) {tuple(map(int, where))}: "
             f"error/tolerance = {ratio:.3f}; largest errors R={errs['R']:.3e} V={errs['V']:.3e} "
             f"tau={errs['tau']:.3e}, flat bound {tolerance(n):.3e}")
+    MARGINS.append(line)
     return out
