@@ -33,7 +33,7 @@ hipError_t launch_panel_seq(float* H, int64_t sHb, int64_t ldh, int J0, int nblk
 size_t cq_workspace_floats(int batch);
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
-                           int64_t sTwb, float* ws, int batch, bool fused, bool one_pass,
+                           int64_t sTwb, float* ws, int batch, bool fused, int one_pass,
                            hipStream_t stream);
 const int* cq_flags(float* ws, int batch);
 size_t cq_flags_offset_floats(int batch);
@@ -93,7 +93,7 @@ int outer_blocks(const qr_options& o) { return o.outer_panels ? o.outer_panels :
 bool options_valid(const qr_options& o) {
   return (o.cholqr == 0 || o.cholqr == 1) &&
          (o.cholqr_min_rows == 0 || (o.cholqr_min_rows >= 65 && o.cholqr_min_rows <= kMaxN)) &&
-         (o.cholqr_one_pass == 0 || o.cholqr_one_pass == 1) &&
+         (o.cholqr_one_pass >= 0 && o.cholqr_one_pass <= 2) &&
          (o.cholqr_fused == 0 || o.cholqr_fused == 1) && (o.lookahead == 0 || o.lookahead == 1) &&
          o.outer_panels >= 0 && o.outer_panels <= kMaxBlocks;
 }
@@ -226,7 +226,7 @@ hipError_t run_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, i
   const double bytes = 4.0 * r * 64.0 * 4.0 * batch;
   return traced(QR_KERNEL_CHOLQR, flops, bytes, s, [&] {
     return qr::launch_cq_block(Src, sSb, lds, Hb, sHb, ldh, r, tau, sTaub, T, sTb, ws, batch,
-                               o.cholqr_fused != 0, o.cholqr_one_pass != 0, s);
+                               o.cholqr_fused != 0, o.cholqr_one_pass, s);
   });
 }
 

@@ -457,13 +457,14 @@ __device__ __forceinline__ void cq_store_rows(float* __restrict__ Z, int64_t ldz
 // ---------------------------------------------------------------------------
 // Pass 1 per matrix: scaled Cholesky of G1, guard, M1 = R1^-1 and R1 into the
 // workspace (mats[b]: M1 at 0, R1 at kCqMat), flag[b] = kCqFlagTwo,
-// kCqFlagSingle (one pass is enough; only with allow_single) or
-// kCqFlagFallback.
+// kCqFlagSingle (one pass is enough; only with allow_single >= 1) or
+// kCqFlagFallback (also, with allow_single = 2, a matrix that would need the
+// second pass).
 constexpr int kCqChol1Lds = 2 * kCqB * kCqLS + 4 * 64 + 16;  // floats
 __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
                                               const float* __restrict__ part, int nchunk,
                                               float* __restrict__ mats, int64_t sMb,
-                                              int* __restrict__ flags, bool allow_single) {
+                                              int* __restrict__ flags, int allow_single) {
   float* const G = smem;
   float* const Ri = G + kCqB * kCqLS;
   float* const piv = Ri + kCqB * kCqLS;
@@ -528,8 +529,11 @@ __device__ __forceinline__ void cq_chol1_body(float* __restrict__ smem, int b,
     // 128; 2.7e-6 and 1.3e-5 at r = 1024), under the parity tolerance 4 r eps32
     // (6.1e-5 at r = 128).
     const float ssum = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
-    const bool single = allow_single && ssum <= kCqSingleMaxF2;
-    if (j == 0) flags[b] = ok ? (single ? kCqFlagSingle : kCqFlagTwo) : kCqFlagFallback;
+    const bool single = allow_single != 0 && ssum <= kCqSingleMaxF2;
+    const bool two_ok = allow_single != 2;
+    if (j == 0)
+      flags[b] = ok ? (single ? kCqFlagSingle : (two_ok ? kCqFlagTwo : kCqFlagFallback))
+                    : kCqFlagFallback;
   }
 }
 
@@ -783,7 +787,7 @@ __global__ __launch_bounds__(64 * kCqGramWaves(kFused)) void k_cq_gram(const flo
     cq_recon_body(smem, b, part, nchunk, mats, sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau,
                   sTaub, Tws, sTwb);
   else
-    cq_chol1_body(smem, b, part, nchunk, mats, sMb, flags, false);  // two passes
+    cq_chol1_body(smem, b, part, nchunk, mats, sMb, flags, 0);  // two passes
 }
 
 // The per-matrix steps as kernels of their own (one workgroup per matrix),
@@ -792,7 +796,7 @@ __global__ __launch_bounds__(256) void k_cq_chol1(const float* __restrict__ part
                                                   float* __restrict__ mats, int64_t sMb,
                                                   int* __restrict__ flags, int allow_single) {
   __shared__ __attribute__((aligned(16))) float smem[kCqChol1Lds + 8];
-  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, allow_single != 0);
+  cq_chol1_body(smem, blockIdx.x, part, nchunk, mats, sMb, flags, allow_single);
 }
 
 __global__ __launch_bounds__(256) void k_cq_recon(const float* __restrict__ part, int nchunk,
@@ -879,7 +883,7 @@ size_t cq_workspace_floats(int batch) {
 // element of matrix 0; ws holds cq_workspace_floats(batch) floats.
 hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb, int64_t sHb,
                            int64_t ldh, int r, float* tau, int64_t sTaub, float* Tws,
-                           int64_t sTwb, float* ws, int batch, bool fused, bool one_pass,
+                           int64_t sTwb, float* ws, int batch, bool fused, int one_pass,
                            hipStream_t stream) {
   if (r <= kCqB || r > kMaxStripRows || batch < 1) return hipErrorInvalidValue;
   const int gw = kCqGramWaves(fused);
@@ -904,9 +908,13 @@ hipError_t launch_cq_block(const float* Src, int64_t sSb, int64_t lds, float* Hb
                        r, rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws,
                        sTwb);
     hipLaunchKernelGGL(k_cq_chol1, dim3(batch), dim3(256), 0, stream, (const float*)part, nc,
-                       mats, sMb, flags, one_pass ? 1 : 0);
-    hipLaunchKernelGGL((k_cq_gram<true, false>), dim3(g1), dim3(64 * gw), 0, stream, Src, sSb, lds, r,
-                       rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
+                       mats, sMb, flags, one_pass);
+    // one_pass = 2: no matrix takes the second pass, so its Gram launch (which
+    // would return at once for every matrix) is not made.
+    if (one_pass != 2)
+      hipLaunchKernelGGL((k_cq_gram<true, false>), dim3(g1), dim3(64 * gw), 0, stream, Src, sSb,
+                         lds, r, rc, nc, mats, sMb, part, flags, cnt, Hb, sHb, ldh, tau, sTaub,
+                         Tws, sTwb);
     hipLaunchKernelGGL(k_cq_recon, dim3(batch), dim3(256), 0, stream, (const float*)part, nc, mats,
                        sMb, flags, Src, sSb, lds, Hb, sHb, ldh, tau, sTaub, Tws, sTwb);
   }

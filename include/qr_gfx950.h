@@ -88,8 +88,10 @@ typedef struct qr_options {
                           the CholeskyQR2 route; 0: Householder panels for every block */
   int cholqr_min_rows; /* 0 (default): 128 rows in calls of <= 64 matrices, 512 above;
                           else the row bound itself (>= 65) */
-  int cholqr_one_pass; /* 1 (default): one CholeskyQR pass where ||R1s^-1||_F^2 <= 144;
-                          0: always two */
+  int cholqr_one_pass; /* 1 (default): one CholeskyQR pass where ||R1s^-1||_F^2 <= 144,
+                          else two; 0: always two; 2: one pass only, a matrix that would
+                          need the second takes the Householder panels for that block (no
+                          pass-2 launches). The fused variant always takes two. */
   int cholqr_fused;    /* 0 (default): five launches per block; 1: Gram and per-matrix
                           steps fused (the last workgroup of a matrix does its step) */
   int lookahead;       /* 1 (default): rest of the trailing update on a second stream */

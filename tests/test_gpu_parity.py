@@ -678,6 +678,23 @@ def test_cholqr_one_pass_bound_vs_oracle(oracle, inv_sum, code):
                   what=f"one-pass bound code {code}")
 
 
+def test_cholqr_one_pass_only_sends_two_pass_blocks_to_the_panels(oracle):
+    """cholqr_one_pass = 2: the block just over the one-pass bound, which the
+    default would take in two passes, is factored by the Householder panels
+    instead (route code 1, no pass-2 launch); a Gaussian block still takes
+    one pass. Both match the oracle at the flat tolerance."""
+    n = 160
+    _say("cholqr one pass only, n=160")
+    g = torch.Generator().manual_seed(43)
+    A = torch.randn(2, n, n, generator=g)
+    blk, _ = near_bound_block(n, 152.0, seed=0)
+    A[0, :, :64] = torch.from_numpy(blk)
+    H, tau, codes = _run_ws(A, cholqr_one_pass=2)
+    assert codes.tolist() == [1, 2], codes
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="one pass only")
+
+
 @pytest.mark.parametrize("n", [300, 2048])
 def test_cholqr_forced_two_passes_vs_oracle(oracle, n):
     """The first block of a Gaussian matrix (the only route block with

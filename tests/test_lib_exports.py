@@ -111,7 +111,8 @@ def test_route_options_defaults_and_validation(lib):
     ex = lib.qr_geqrf_f32_ex
     assert ex(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, None, None) == 3  # NULL: defaults
     for field, bad in (("cholqr", 2), ("cholqr_min_rows", 64), ("cholqr_min_rows", 5000),
-                       ("cholqr_one_pass", -1), ("cholqr_fused", 2), ("lookahead", 7),
+                       ("cholqr_one_pass", -1), ("cholqr_one_pass", 3), ("cholqr_fused", 2),
+                       ("lookahead", 7),
                        ("outer_panels", 9), ("outer_panels", -1)):
         o = _lib.default_options()
         setattr(o, field, bad)
