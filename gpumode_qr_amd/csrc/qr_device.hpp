@@ -169,6 +169,21 @@ __device__ __forceinline__ void dot4_bcast16(float& a0, float& a1, float& a2, fl
       : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J));
 }
 
+// a_v = x_v[J] * x_v for v < 4: dot4_bcast16's first term, written instead of
+// accumulated (no zeroed accumulators needed).
+template <int J>
+__device__ __forceinline__ void dot4_bcast16_first(float& a0, float& a1, float& a2, float& a3,
+                                                   float x0, float x1, float x2, float x3) {
+  static_assert(J >= 0 && J < 16, "row_newbcast lane");
+  asm("s_nop 4\n\t"
+      "v_mul_f32_dpp %0, %4, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_mul_f32_dpp %1, %5, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_mul_f32_dpp %2, %6, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_mul_f32_dpp %3, %7, %7 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(a3)
+      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J));
+}
+
 // x_v += x_v[J] * s for v < 4 (same broadcast and wait states as dot4_bcast16).
 // Each instruction reads its DPP source before writing it, and no instruction
 // reads a register written by the one before it.
@@ -249,6 +264,20 @@ __device__ __forceinline__ float rows16_sum(float x) {
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false,
                                                   false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Row group GJ's value (lane k + 16 GJ) in every row group's lane k, by the
+// same two swaps without adds: permlane16_swap(x, x) gives [x0, x0, x2, x2]
+// and [x1, x1, x3, x3] (16-lane rows), permlane32_swap(y, y) of y = [p, p, q, q]
+// gives [p, p, p, p] and [q, q, q, q].
+template <int GJ>
+__device__ __forceinline__ float rows16_bcast(float x) {
+  static_assert(GJ >= 0 && GJ < 4, "row group");
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const unsigned y = (GJ & 1) ? a[1] : a[0];
+  const auto b = __builtin_amdgcn_permlane32_swap(y, y, false, false);
+  return __uint_as_float((GJ & 2) ? b[1] : b[0]);
 }
 
 __device__ __forceinline__ float rows16_max(float x) {

@@ -87,26 +87,55 @@ struct SmallnCol {
 
 // Column JQ of T: T[k][JQ] = -tau_JQ sum_{q < JQ} T[k][q] z_q for k < JQ, with
 // z_q = V_q^T v_JQ stored in zb[JQ] by the lanes q during column step JQ. Run
-// one step later, off that step's critical path; LDS operations of one wave
-// are performed in program order, so the stores are visible.
+// one step later, off that step's critical path, in two parts: the LDS reads
+// at the start of step JQ + 1 (LDS operations of one wave are performed in
+// program order, so the stores are visible) and the products at its end, so
+// that the reads' latency hides behind the step instead of stalling it.
+// Exactly the JQ values z_0 .. z_{JQ-1} are read (b128, b64, b32 pieces): a
+// register loaded but never used would be reallocated at once, and its write
+// would make the wave wait for the read there.
+template <int JQ>
+struct SmalnTz {
+  float z[JQ > 0 ? JQ : 1];
+};
+
 template <int S, int JQ>
-__device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShared<S>& sh, int k) {
+__device__ __forceinline__ void smalln_t_load(SmalnTz<JQ>& tz, const SmallnShared<S>& sh) {
+  if constexpr (JQ > 0) {
+#pragma unroll
+    for (int q4 = 0; q4 < JQ / 4; ++q4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sh.zb[JQ][4 * q4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tz.z[4 * q4 + e] = v[e];
+    }
+    constexpr int q0 = JQ & ~3;
+    if constexpr ((JQ & 3) >= 2) {
+      const float2 v = *reinterpret_cast<const float2*>(&sh.zb[JQ][q0]);
+      tz.z[q0] = v.x;
+      tz.z[q0 + 1] = v.y;
+    }
+    if constexpr (JQ & 1) tz.z[JQ - 1] = sh.zb[JQ][JQ - 1];
+  }
+}
+
+template <int JQ>
+__device__ __forceinline__ void smalln_t_finish(SmallnCol& col, const SmalnTz<JQ>& tz, int k) {
   if constexpr (JQ > 0) {
     float sa = 0.0f, sb = 0.0f;
 #pragma unroll
-    for (int q4 = 0; q4 < (JQ + 3) / 4; ++q4) {
-      const f32x4 z = *reinterpret_cast<const f32x4*>(&sh.zb[JQ][4 * q4]);
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int q = 4 * q4 + e4;
-        if (q < JQ) {
-          if (q & 1) sb = fmaf(col.trow[q], z[e4], sb);
-          else sa = fmaf(col.trow[q], z[e4], sa);
-        }
-      }
+    for (int q = 0; q < JQ; ++q) {
+      if (q & 1) sb = fmaf(col.trow[q], tz.z[q], sb);
+      else sa = fmaf(col.trow[q], tz.z[q], sa);
     }
     col.trow[JQ] = (k < JQ) ? -col.prev_tau * (sa + sb) : col.trow[JQ];
   }
+}
+
+template <int S, int JQ>
+__device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShared<S>& sh, int k) {
+  SmalnTz<JQ> tz;
+  smalln_t_load<S, JQ>(tz, sh);
+  smalln_t_finish<JQ>(col, tz, k);
 }
 
 // Column step JJ of panel P (column j = 16 P + JJ): reflector of column j and
@@ -131,7 +160,9 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   int k = k0, g = g0;
   asm volatile("" : "+v"(k), "+v"(g));
   const bool upd = (k > JJ) && kin;
-  if constexpr (JJ > 0) smalln_t_column<S, JJ - 1>(col, sh, k);
+  constexpr int JT = JJ > 0 ? JJ - 1 : 0;  // column of T finished in this step
+  SmalnTz<JT> tz;
+  if constexpr (JJ > 0) smalln_t_load<S, JT>(tz, sh);
 
   // x = column j below the diagonal (rows <= j masked), broadcast from lane JJ
   // of every 16-lane row; partial dot with this lane's column. Rows <= j all
@@ -142,18 +173,31 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   // mask of the fused broadcast (dot4_bcast16_below), not by selects.
   constexpr int NX = kSafe ? NT : 1;
   float xb[NX][4];
-  float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float dv[4];
+  if constexpr (!kSafe) {
+    // Tiles 1.. first (the first one writes dv, so no zeroing), then tile 0,
+    // whose masked rows keep the sum of the others.
+    if constexpr (NT >= 2) {
+      dot4_bcast16_first<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + 1)],
+                             c[P][4 * (P + 1) + 1], c[P][4 * (P + 1) + 2],
+                             c[P][4 * (P + 1) + 3]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dv[v] = 0.0f;
+    }
+#pragma unroll
+    for (int t = 2; t < NT; ++t)
+      dot4_bcast16<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
+                       c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3]);
+    dot4_bcast16_below<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * P], c[P][4 * P + 1],
+                           c[P][4 * P + 2], c[P][4 * P + 3]);
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dv[v] = 0.0f;
+  }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    if constexpr (!kSafe) {
-      if (t == 0)
-        dot4_bcast16_below<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * P], c[P][4 * P + 1],
-                               c[P][4 * P + 2], c[P][4 * P + 3]);
-      else
-        dot4_bcast16<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
-                         c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3]);
-      continue;
-    }
+    if constexpr (!kSafe) continue;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float own = c[P][4 * (P + t) + v];
@@ -168,9 +212,8 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   // run beside them.
   const float dsum = (dv[0] + dv[1]) + (dv[2] + dv[3]);
   const float alpha = readlane_f(c[P][4 * P + vj], JJ + 16 * gj);
-  const float ev = (g == gj) ? c[P][4 * P + vj] : 0.0f;  // row j of this column
   const float ds = rows16_sum(dsum);
-  const float e = rows16_sum(ev);
+  const float e = rows16_bcast<gj>(c[P][4 * P + vj]);  // row j of this column
 #if QR_SMALLN_SIGMA_FROM_DS
   const float sigma = readlane_f(ds, JJ);  // lane JJ's dot is x^T x
 #else
@@ -236,6 +279,12 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     }
     if (upd && g == gj) c[P][4 * P + vj] -= cc;
   }
+  if constexpr (JJ > 0) {
+    // Keep the products here, after the step's own work: hoisted next to
+    // their LDS reads, they would make the step wait for those reads first.
+    __builtin_amdgcn_sched_barrier(0);
+    smalln_t_finish<JT>(col, tz, k);
+  }
   // Column j of T needs z_q = V_q^T v_j = ((c_q[j] + (x^T c_q pre) gamma) pre_q)
   // gamma_q for the panel's q < j (c_q still holds the raw x_q). Every row
   // group stores the same value.
@@ -253,7 +302,7 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
 template <int S, bool kVec>
 // At least two waves per SIMD (<= 256 VGPRs): 2048 matrices fill every SIMD
 // twice, and the second wave hides the first one's per-column latency.
-__global__ __launch_bounds__(64 * kSnWaves, 2) void k_geqrf_smalln(
+__global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
     const float* __restrict__ A, int64_t sAb, int64_t sAr, int64_t sAc, float* __restrict__ H,
     float* __restrict__ tau, int batch, int n) {
   __shared__ __align__(16) SmallnShared<S> shm[kSnWaves];
@@ -267,32 +316,36 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) void k_geqrf_smalln(
   const float* Ab = A + (int64_t)b * sAb;
 
   float c[S][4 * S];
-  if constexpr (kVec) {
-    // n = 16 S, unit column stride, 16-byte aligned rows: every lane loads
-    // S^2 16-byte row pieces (16 lanes cover a 64-float row, so each load
-    // instruction reads 4 whole rows), then each 16-row tile is transposed to
-    // the strip layout through LDS (row pitch 16 S + 4: conflict-free reads).
-    static_assert(S == 4, "vectorised load is laid out for 64 x 64");
-    constexpr int kPitch = 16 * S + 4;
-    f32x4 q[S][4];
+  // kVec: n = 16 S, unit column stride, 16-byte aligned rows. Each load
+  // instruction reads 16 rows of one strip (lane l: row 16 rb + l / 4, columns
+  // 16 s + 4 (l % 4) .. +3; 1 KB), strip 0 first; a strip is transposed to the
+  // strip layout through a per-wave LDS tile (row pitch kSnVStride:
+  // conflict-free reads). Strip 0 is transposed at once; strips 1 .. S-1 only
+  // after panel 0's column steps, which so overlap their loads.
+  static_assert(!kVec || S == 4, "vectorised load is laid out for 64 x 64");
+  f32x4 q[kVec ? S : 1][4];
+  auto transpose_strip = [&](auto SI) {
+    constexpr int s = decltype(SI)::value;
+    const int lr = lane >> 2, lc = 4 * (lane & 3);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+      *reinterpret_cast<f32x4*>(&sh.vt[(16 * rb + lr) * kSnVStride + lc]) = q[s][rb];
+    wave_lds_sync();
 #pragma unroll
     for (int t = 0; t < S; ++t)
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        q[t][m] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)(16 * t + 4 * m + g) * sAr +
-                                                  4 * k);
+      for (int v = 0; v < 4; ++v) c[s][4 * t + v] = sh.vt[(16 * t + 4 * g + v) * kSnVStride + k];
+    wave_lds_sync();
+  };
+  if constexpr (kVec) {
+    const int lr = lane >> 2, lc = 4 * (lane & 3);
 #pragma unroll
-    for (int t = 0; t < S; ++t) {
+    for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        *reinterpret_cast<f32x4*>(&sh.save[(4 * m + g) * kPitch + 4 * k]) = q[t][m];
-      wave_lds_sync();
-#pragma unroll
-      for (int s2 = 0; s2 < S; ++s2)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) c[s2][4 * t + v] = sh.save[(4 * g + v) * kPitch + 16 * s2 + k];
-      wave_lds_sync();
-    }
+      for (int rb = 0; rb < 4; ++rb)
+        q[s][rb] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)(16 * rb + lr) * sAr + 16 * s +
+                                                   lc);
+    transpose_strip(std::integral_constant<int, 0>{});
   } else {
   // Branch-free loads: out-of-range rows/columns read a clamped (valid)
   // address and are replaced by zero, so the 16 S^2 loads issue back to back.
@@ -313,6 +366,28 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) void k_geqrf_smalln(
       }
   });
   }
+
+  // Strip s of H, stored as soon as its panel is packed (no later step
+  // touches it), so the stores of strips 0 .. S-2 overlap the later panels.
+  float* Hb = H + (int64_t)b * n * n + (int64_t)(4 * g) * n + k;
+  auto store_strip = [&](auto SI) {
+    constexpr int s = decltype(SI)::value;
+    if (n == 16 * S) {
+#pragma unroll
+      for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
+    } else {
+      int kk = k0, gg = g0;
+      asm volatile("" : "+v"(kk), "+v"(gg));
+#pragma unroll
+      for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (16 * t + 4 * gg + v < n && 16 * s + kk < n)
+            Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
+    }
+  };
 
   static_for<0, S>([&](auto PI) {
     constexpr int p = decltype(PI)::value;
@@ -368,6 +443,10 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) void k_geqrf_smalln(
         const float x = c[p][4 * t + v];
         c[p][4 * t + v] = (row < kd) ? x : ((row == kd) ? my_beta : (x * my_pre) * my_gamma);
       }
+
+    store_strip(PI);
+    if constexpr (kVec && p == 0)
+      static_for<1, S>([&](auto SI) { transpose_strip(SI); });
 
     if constexpr (p + 1 < S) {
       // T (16 x 16, upper), row k in lane k: to the accumulator layout via LDS.
@@ -444,28 +523,6 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) void k_geqrf_smalln(
     }
   });
 
-  float* Hb = H + (int64_t)b * n * n + (int64_t)(4 * g) * n + k;
-  if (n == 16 * S) {
-    static_for<0, S>([&](auto SI) {
-      constexpr int s = decltype(SI)::value;
-#pragma unroll
-      for (int t = 0; t < S; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
-    });
-  } else {
-    int kk = k0, gg = g0;
-    asm volatile("" : "+v"(kk), "+v"(gg));
-    static_for<0, S>([&](auto SI) {
-      constexpr int s = decltype(SI)::value;
-#pragma unroll
-      for (int t = 0; t < S; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (16 * t + 4 * gg + v < n && 16 * s + kk < n)
-            Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
-    });
-  }
 }
 
 // Host-side dispatch over the number of 16-column strips. H is (batch, n, n)
