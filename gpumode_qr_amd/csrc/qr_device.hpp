@@ -37,6 +37,22 @@ __device__ __forceinline__ bool reflector_fast_ok(float alpha, float sigma) {
   return sigma >= kSigmaLo && sigma <= kSigmaHi && fabsf(alpha) <= kAlphaHi;
 }
 
+// reflector_fast_ok on the bit patterns (sigma >= +0 as a sum of squares):
+// for non-negative floats the bits order like the values, and NaN, Inf and
+// -0 fall outside both ranges. On wave-uniform operands these are scalar
+// integer instructions, so the per-column check costs no vector issue slots.
+__device__ __forceinline__ bool reflector_fast_ok_bits(float alpha, float sigma) {
+  constexpr uint32_t lo = 0x0d800000u;  // bits of kSigmaLo = 2^-100
+  constexpr uint32_t hi = 0x71800000u;  // bits of kSigmaHi = 2^100
+  constexpr uint32_t ahi = 0x58800000u; // bits of kAlphaHi = 2^50
+  static_assert(__builtin_bit_cast(uint32_t, kSigmaLo) == lo, "2^-100");
+  static_assert(__builtin_bit_cast(uint32_t, kSigmaHi) == hi, "2^100");
+  static_assert(__builtin_bit_cast(uint32_t, kAlphaHi) == ahi, "2^50");
+  const uint32_t sb = __float_as_uint(sigma);
+  const uint32_t ab = __float_as_uint(alpha) & 0x7fffffffu;
+  return (sb - lo) <= (hi - lo) && ab <= ahi;
+}
+
 // 1/x from v_rcp_f32 plus one Newton step (about 0.5 ulp) for normal x.
 __device__ __forceinline__ float rcp_nr(float x) {
   const float r = __builtin_amdgcn_rcpf(x);

@@ -228,7 +228,7 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   Reflector R;
   float wk;
   if constexpr (!kSafe) {
-    ok = ok && (identity || reflector_fast_ok(alpha, sigma));
+    ok = ok && (identity || reflector_fast_ok_bits(alpha, sigma));
     R = reflector_fast_rcp(alpha, identity ? 1.0f : sigma);
     if (identity) R = reflector_identity(alpha);
     // v^T c_k = c_k[j] + gamma x^T c_k;  c_k -= tau (v^T c_k) v.
