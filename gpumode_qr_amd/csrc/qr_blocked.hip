@@ -108,7 +108,7 @@ __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, 
     const float sigma = readlane_f(ds, J);
     const float alpha = readlane_f(e, J);
     const bool ident = dj >= r - 1;  // no rows below the diagonal
-    ok = ok && (ident || reflector_fast_ok(alpha, sigma));
+    ok = ok && (ident || reflector_fast_ok_bits(alpha, sigma));
     Reflector R = reflector_fast_rcp(alpha, sigma);
     if (ident) R = reflector_identity(alpha);
     const float wk = fmaf(R.gamma, ds, e);  // v_J^T c_k

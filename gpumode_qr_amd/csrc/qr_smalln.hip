@@ -149,7 +149,7 @@ __device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShar
 // such columns: v = (x pre) gamma with the power-of-two prescale `pre`.
 template <int S, int P, int JJ, bool kSafe>
 __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S>& sh, int k0,
-                                            int g0, int n, bool kin, bool& ok,
+                                            int g0, int n, bool kin, int& bad,
                                             SmallnCol& col) {
   constexpr int NT = S - P;  // row tiles at or below the panel's diagonal tile
   constexpr int gj = JJ >> 2, vj = JJ & 3;
@@ -228,7 +228,9 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   Reflector R;
   float wk;
   if constexpr (!kSafe) {
-    ok = ok && (identity || reflector_fast_ok_bits(alpha, sigma));
+    // Wave-uniform integer flag (a scalar register; a bool here ends up as a
+    // per-lane 0/1 value moved back and forth every step).
+    bad |= (identity || reflector_fast_ok_bits(alpha, sigma)) ? 0 : 1;
     R = reflector_fast_rcp(alpha, identity ? 1.0f : sigma);
     if (identity) R = reflector_identity(alpha);
     // v^T c_k = c_k[j] + gamma x^T c_k;  c_k -= tau (v^T c_k) v.
@@ -288,7 +290,8 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   // Column j of T needs z_q = V_q^T v_j = ((c_q[j] + (x^T c_q pre) gamma) pre_q)
   // gamma_q for the panel's q < j (c_q still holds the raw x_q). Every row
   // group stores the same value.
-  sh.zb[JJ][k] = (k < JJ) ? (wk * col.pre) * col.gamma : 0.0f;
+  // (Entries k >= JJ are never read.)
+  sh.zb[JJ][k] = (wk * col.pre) * col.gamma;
   if (k == JJ) {
     col.beta = R.beta;
     col.gamma = R.gamma;
@@ -403,12 +406,12 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_e
           f32x4{c[p][4 * (p + t)], c[p][4 * (p + t) + 1], c[p][4 * (p + t) + 2],
                 c[p][4 * (p + t) + 3]};
     SmallnCol col;
-    bool ok = true;
+    int bad = 0;
     static_for<0, 16>([&](auto JI) {
       constexpr int jj = decltype(JI)::value;
-      if (jj < kw) smalln_step<S, p, jj, false>(c, sh, k0, g0, n, kin, ok, col);
+      if (jj < kw) smalln_step<S, p, jj, false>(c, sh, k0, g0, n, kin, bad, col);
     });
-    if (!ok) [[unlikely]] {
+    if (__builtin_amdgcn_readfirstlane(bad)) [[unlikely]] {
       wave_lds_sync();
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_e
         for (int v = 0; v < 4; ++v) c[p][4 * (p + t) + v] = sv[v];
       }
       col = SmallnCol();
-      bool unused = true;
+      int unused = 0;
       static_for<0, 16>([&](auto JI) {
         constexpr int jj = decltype(JI)::value;
         if (jj < kw) smalln_step<S, p, jj, true>(c, sh, k0, g0, n, kin, unused, col);
