@@ -84,7 +84,7 @@ __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, 
   using S = Strip<NW, RL>;
   const int k = lane & 15, g = lane >> 4;
   const int d0 = 16 * p;
-  bool ok = true;
+  int bad = 0;  // wave-uniform integer flag (a bool becomes a per-lane 0/1 here)
   static_for<0, 16>([&](auto jc) __attribute__((always_inline)) {
     constexpr int J = decltype(jc)::value;
     if (J >= kw) return;
@@ -108,7 +108,7 @@ __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, 
     const float sigma = readlane_f(ds, J);
     const float alpha = readlane_f(e, J);
     const bool ident = dj >= r - 1;  // no rows below the diagonal
-    ok = ok && (ident || reflector_fast_ok_bits(alpha, sigma));
+    bad |= (ident || reflector_fast_ok_bits(alpha, sigma)) ? 0 : 1;
     Reflector R = reflector_fast_rcp(alpha, sigma);
     if (ident) R = reflector_identity(alpha);
     const float wk = fmaf(R.gamma, ds, e);  // v_J^T c_k
@@ -133,7 +133,7 @@ __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, 
       st.tau = R.tau;
     }
   });
-  return ok;
+  return __builtin_amdgcn_readfirstlane(bad) == 0;
 }
 
 // General pass: the same steps for any column (slarfg's zero-norm and
