@@ -169,50 +169,52 @@ __device__ __forceinline__ float row_bcast16_nocse(float v) {
 
 // a_v += x_v[J] * x_v for v < 4, where x_v[J] is x_v in lane J of the lane's
 // 16-lane row (DPP row_newbcast folded into v_fmac_f32, which the compiler does
-// not form by itself). The leading s_nop 4 gives the wait states a DPP source
-// needs after a VALU write of that register or of EXEC; the compiler's hazard
-// tracking does not look inside inline asm.
-template <int J>
+// not form by itself). The compiler's hazard tracking does not look inside
+// inline asm, so each block starts with s_nop kNop (kNop + 1 wait states):
+// the default 4 covers a VALU write of EXEC (5 wait states before a DPP
+// instruction); 1 covers a VALU write of a source register (2), for callers
+// with no VALU write of EXEC and no MFMA result read first by these blocks.
+template <int J, int kNop = 4>
 __device__ __forceinline__ void dot4_bcast16(float& a0, float& a1, float& a2, float& a3, float x0,
                                              float x1, float x2, float x3) {
   static_assert(J >= 0 && J < 16, "row_newbcast lane");
-  asm("s_nop 4\n\t"
+  asm("s_nop %c[nop]\n\t"
       "v_fmac_f32_dpp %0, %4, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %1, %5, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %2, %6, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %3, %7, %7 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
       : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)
-      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J));
+      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J), [nop] "i"(kNop));
 }
 
 // a_v = x_v[J] * x_v for v < 4: dot4_bcast16's first term, written instead of
 // accumulated (no zeroed accumulators needed).
-template <int J>
+template <int J, int kNop = 4>
 __device__ __forceinline__ void dot4_bcast16_first(float& a0, float& a1, float& a2, float& a3,
                                                    float x0, float x1, float x2, float x3) {
   static_assert(J >= 0 && J < 16, "row_newbcast lane");
-  asm("s_nop 4\n\t"
+  asm("s_nop %c[nop]\n\t"
       "v_mul_f32_dpp %0, %4, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_mul_f32_dpp %1, %5, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_mul_f32_dpp %2, %6, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_mul_f32_dpp %3, %7, %7 row_newbcast:%8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
       : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(a3)
-      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J));
+      : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J), [nop] "i"(kNop));
 }
 
 // x_v += x_v[J] * s for v < 4 (same broadcast and wait states as dot4_bcast16).
 // Each instruction reads its DPP source before writing it, and no instruction
 // reads a register written by the one before it.
-template <int J>
+template <int J, int kNop = 4>
 __device__ __forceinline__ void axpy4_bcast16(float& x0, float& x1, float& x2, float& x3, float s) {
   static_assert(J >= 0 && J < 16, "row_newbcast lane");
-  asm("s_nop 4\n\t"
+  asm("s_nop %c[nop]\n\t"
       "v_fmac_f32_dpp %0, %0, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %1, %1, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %2, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %3, %3, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf bound_ctrl:1"
       : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
-      : "v"(s), "i"(J));
+      : "v"(s), "i"(J), [nop] "i"(kNop));
 }
 
 // Row mask of the 16-lane rows g whose row 4 g + v of a 16-row tile lies below
@@ -225,11 +227,11 @@ constexpr int rows_below_mask() {
 // dot4_bcast16 for the tile that holds row J: a_v += x_v[J] x_v only in the
 // rows below row J (rows_below_mask); the other rows keep a_v. DPP's row mask
 // gates the destination write, not the source read.
-template <int J>
+template <int J, int kNop = 4>
 __device__ __forceinline__ void dot4_bcast16_below(float& a0, float& a1, float& a2, float& a3,
                                                    float x0, float x1, float x2, float x3) {
   static_assert(J >= 0 && J < 16, "row_newbcast lane");
-  asm("s_nop 4\n\t"
+  asm("s_nop %c[nop]\n\t"
       "v_fmac_f32_dpp %0, %4, %4 row_newbcast:%8 row_mask:%9 bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %1, %5, %5 row_newbcast:%8 row_mask:%10 bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %2, %6, %6 row_newbcast:%8 row_mask:%11 bank_mask:0xf bound_ctrl:1\n\t"
@@ -237,23 +239,23 @@ __device__ __forceinline__ void dot4_bcast16_below(float& a0, float& a1, float& 
       : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)
       : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "i"(J), "i"(rows_below_mask<J, 0>()),
         "i"(rows_below_mask<J, 1>()), "i"(rows_below_mask<J, 2>()),
-        "i"(rows_below_mask<J, 3>()));
+        "i"(rows_below_mask<J, 3>()), [nop] "i"(kNop));
 }
 
 // axpy4_bcast16 for the tile that holds row J: x_v += x_v[J] s only in the rows
 // below row J.
-template <int J>
+template <int J, int kNop = 4>
 __device__ __forceinline__ void axpy4_bcast16_below(float& x0, float& x1, float& x2, float& x3,
                                                     float s) {
   static_assert(J >= 0 && J < 16, "row_newbcast lane");
-  asm("s_nop 4\n\t"
+  asm("s_nop %c[nop]\n\t"
       "v_fmac_f32_dpp %0, %0, %4 row_newbcast:%5 row_mask:%6 bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %1, %1, %4 row_newbcast:%5 row_mask:%7 bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %2, %2, %4 row_newbcast:%5 row_mask:%8 bank_mask:0xf bound_ctrl:1\n\t"
       "v_fmac_f32_dpp %3, %3, %4 row_newbcast:%5 row_mask:%9 bank_mask:0xf bound_ctrl:1"
       : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
       : "v"(s), "i"(J), "i"(rows_below_mask<J, 0>()), "i"(rows_below_mask<J, 1>()),
-        "i"(rows_below_mask<J, 2>()), "i"(rows_below_mask<J, 3>()));
+        "i"(rows_below_mask<J, 2>()), "i"(rows_below_mask<J, 3>()), [nop] "i"(kNop));
 }
 
 // Sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
@@ -303,6 +305,38 @@ __device__ __forceinline__ float rows16_max(float x) {
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false,
                                                   false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Lane masks of the 16 x 4 strip layout (lane l: column k = l & 15, row group
+// g = l >> 4) as compile-time constants. lane_in(mask) is the lane's bit of a
+// wave-uniform mask: a select on it reads the mask from an SGPR pair (set by
+// scalar moves) instead of a per-lane compare.
+constexpr uint64_t lanes_k_gt(int j) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((l & 15) > j) m |= uint64_t(1) << l;
+  return m;
+}
+constexpr uint64_t lanes_k_eq(int j) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((l & 15) == j) m |= uint64_t(1) << l;
+  return m;
+}
+constexpr uint64_t lanes_g_eq(int g) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((l >> 4) == g) m |= uint64_t(1) << l;
+  return m;
+}
+constexpr uint64_t lanes_g_ge(int g) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((l >> 4) >= g) m |= uint64_t(1) << l;
+  return m;
+}
+__device__ __forceinline__ bool lane_in(uint64_t mask) {
+  return __builtin_amdgcn_inverse_ballot_w64(mask);
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).

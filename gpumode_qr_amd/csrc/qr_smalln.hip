@@ -30,6 +30,11 @@ constexpr int kSnWaves = 4;     // matrices (one per wave) per workgroup
 #define QR_SMALLN_SIGMA_FROM_DS 1
 #endif
 constexpr int kSnVStride = 20;  // row stride of the V transpose buffer (floats)
+// Wait states before each fused-DPP asm block of the column steps: 1 (two
+// wait states) is what a DPP source written by the previous VALU instruction
+// needs. No VALU instruction of this kernel writes EXEC, and a panel's MFMA
+// results are first read by the panel's save stores, before any step.
+constexpr int kSnNop = 1;
 
 template <int S>
 struct SmallnShared {
@@ -118,8 +123,13 @@ __device__ __forceinline__ void smalln_t_load(SmalnTz<JQ>& tz, const SmallnShare
   }
 }
 
+// Lanes k >= JQ need no select: their entries T[k][q < JQ] are still zero
+// (row k of T is upper triangular, and |z_q| <= 64 since no reflector entry
+// exceeds 1 in magnitude), so their sum
+// is exactly zero and the fma leaves T[k][JQ] (0, or tau_JQ on the diagonal)
+// as it was. Lanes k < JQ hold T[k][JQ] = 0 before: the fma is the product.
 template <int JQ>
-__device__ __forceinline__ void smalln_t_finish(SmallnCol& col, const SmalnTz<JQ>& tz, int k) {
+__device__ __forceinline__ void smalln_t_finish(SmallnCol& col, const SmalnTz<JQ>& tz) {
   if constexpr (JQ > 0) {
     float sa = 0.0f, sb = 0.0f;
 #pragma unroll
@@ -127,15 +137,15 @@ __device__ __forceinline__ void smalln_t_finish(SmallnCol& col, const SmalnTz<JQ
       if (q & 1) sb = fmaf(col.trow[q], tz.z[q], sb);
       else sa = fmaf(col.trow[q], tz.z[q], sa);
     }
-    col.trow[JQ] = (k < JQ) ? -col.prev_tau * (sa + sb) : col.trow[JQ];
+    col.trow[JQ] = fmaf(-col.prev_tau, sa + sb, col.trow[JQ]);
   }
 }
 
 template <int S, int JQ>
-__device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShared<S>& sh, int k) {
+__device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShared<S>& sh) {
   SmalnTz<JQ> tz;
   smalln_t_load<S, JQ>(tz, sh);
-  smalln_t_finish<JQ>(col, tz, k);
+  smalln_t_finish<JQ>(col, tz);
 }
 
 // Column step JJ of panel P (column j = 16 P + JJ): reflector of column j and
@@ -147,19 +157,20 @@ __device__ __forceinline__ void smalln_t_column(SmallnCol& col, const SmallnShar
 // `ok` and leaves garbage; the caller then restores the panel and re-runs it
 // with kSafe = true, which takes slarfg's general path (zero, tiny, huge) for
 // such columns: v = (x pre) gamma with the power-of-two prescale `pre`.
+//
+// Lane conditions are compile-time masks (lanes_*), ANDed with kin_mask (the
+// lanes whose column exists): selects on them take an SGPR pair, no compare.
+// zrow = &sh.zb[0][k] of this lane.
 template <int S, int P, int JJ, bool kSafe, bool kFullN = false>
-__device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S>& sh, int k0,
-                                            int g0, int n, bool kin, int& bad,
+__device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S>& sh,
+                                            float* zrow, int n, uint64_t kin_mask, int& bad,
                                             SmallnCol& col) {
   constexpr int NT = S - P;  // row tiles at or below the panel's diagonal tile
   constexpr int gj = JJ >> 2, vj = JJ & 3;
   const int j = 16 * P + JJ;
-  // Opaque per-step copies of the lane coordinates: the lane-mask compares
-  // below are formed where they are used instead of being hoisted out of all
-  // the unrolled steps into SGPR pairs.
-  int k = k0, g = g0;
-  asm volatile("" : "+v"(k), "+v"(g));
-  const bool upd = (k > JJ) && kin;
+  const bool upd = lane_in(lanes_k_gt(JJ) & kin_mask);
+  const bool upd_row_j = lane_in(lanes_k_gt(JJ) & lanes_g_eq(gj) & kin_mask);
+  const bool is_jj = lane_in(lanes_k_eq(JJ));
   constexpr int JT = JJ > 0 ? JJ - 1 : 0;  // column of T finished in this step
   SmalnTz<JT> tz;
   if constexpr (JJ > 0) smalln_t_load<S, JT>(tz, sh);
@@ -178,7 +189,7 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     // Tiles 1.. first (the first one writes dv, so no zeroing), then tile 0,
     // whose masked rows keep the sum of the others.
     if constexpr (NT >= 2) {
-      dot4_bcast16_first<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + 1)],
+      dot4_bcast16_first<JJ, kSnNop>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + 1)],
                              c[P][4 * (P + 1) + 1], c[P][4 * (P + 1) + 2],
                              c[P][4 * (P + 1) + 3]);
     } else {
@@ -187,10 +198,11 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     }
 #pragma unroll
     for (int t = 2; t < NT; ++t)
-      dot4_bcast16<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
-                       c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3]);
-    dot4_bcast16_below<JJ>(dv[0], dv[1], dv[2], dv[3], c[P][4 * P], c[P][4 * P + 1],
-                           c[P][4 * P + 2], c[P][4 * P + 3]);
+      dot4_bcast16<JJ, kSnNop>(dv[0], dv[1], dv[2], dv[3], c[P][4 * (P + t)],
+                               c[P][4 * (P + t) + 1], c[P][4 * (P + t) + 2],
+                               c[P][4 * (P + t) + 3]);
+    dot4_bcast16_below<JJ, kSnNop>(dv[0], dv[1], dv[2], dv[3], c[P][4 * P], c[P][4 * P + 1],
+                                   c[P][4 * P + 2], c[P][4 * P + 3]);
   } else {
 #pragma unroll
     for (int v = 0; v < 4; ++v) dv[v] = 0.0f;
@@ -201,7 +213,7 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       float own = c[P][4 * (P + t) + v];
-      if (t == 0) own = (g >= (JJ - v + 4) / 4) ? own : 0.0f;  // row 4 g + v > JJ
+      if (t == 0) own = lane_in(lanes_g_ge((JJ - v + 4) / 4)) ? own : 0.0f;  // 4 g + v > JJ
       xb[t < NX ? t : 0][v] = row_bcast16<JJ>(own);
       dv[v] = fmaf(xb[t < NX ? t : 0][v], c[P][4 * (P + t) + v], dv[v]);
     }
@@ -239,12 +251,13 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
     const float ncx = upd ? -(cc * R.gamma) : 0.0f;
     // Tile 0 below row JJ, then tiles 1..: lane JJ (ncx = 0) is never changed,
     // so each broadcast still reads column j's x.
-    axpy4_bcast16_below<JJ>(c[P][4 * P], c[P][4 * P + 1], c[P][4 * P + 2], c[P][4 * P + 3], ncx);
+    axpy4_bcast16_below<JJ, kSnNop>(c[P][4 * P], c[P][4 * P + 1], c[P][4 * P + 2],
+                                    c[P][4 * P + 3], ncx);
 #pragma unroll
     for (int t = 1; t < NT; ++t)
-      axpy4_bcast16<JJ>(c[P][4 * (P + t)], c[P][4 * (P + t) + 1], c[P][4 * (P + t) + 2],
-                        c[P][4 * (P + t) + 3], ncx);
-    if (upd && g == gj) c[P][4 * P + vj] -= cc;
+      axpy4_bcast16<JJ, kSnNop>(c[P][4 * (P + t)], c[P][4 * (P + t) + 1],
+                                c[P][4 * (P + t) + 2], c[P][4 * (P + t) + 3], ncx);
+    c[P][4 * P + vj] = upd_row_j ? c[P][4 * P + vj] - cc : c[P][4 * P + vj];
   } else {
     bool fast = true;
     if (identity) {
@@ -279,33 +292,34 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
         for (int v = 0; v < 4; ++v)
           c[P][4 * (P + t) + v] = fmaf(-cx, (xb[t][v] * R.pre) * R.gamma, c[P][4 * (P + t) + v]);
     }
-    if (upd && g == gj) c[P][4 * P + vj] -= cc;
+    c[P][4 * P + vj] = upd_row_j ? c[P][4 * P + vj] - cc : c[P][4 * P + vj];
   }
   if constexpr (JJ > 0) {
     // Keep the products here, after the step's own work: hoisted next to
     // their LDS reads, they would make the step wait for those reads first.
     __builtin_amdgcn_sched_barrier(0);
-    smalln_t_finish<JT>(col, tz, k);
+    smalln_t_finish<JT>(col, tz);
   }
   // Column j of T needs z_q = V_q^T v_j = ((c_q[j] + (x^T c_q pre) gamma) pre_q)
   // gamma_q for the panel's q < j (c_q still holds the raw x_q). Every row
   // group stores the same value.
   // (Entries k >= JJ are never read.)
-  sh.zb[JJ][k] = (wk * col.pre) * col.gamma;
-  if (k == JJ) {
+  zrow[16 * JJ] = (wk * col.pre) * col.gamma;
+  if (is_jj) {
     col.beta = R.beta;
     col.gamma = R.gamma;
     col.pre = R.pre;
     col.tau = R.tau;
   }
-  col.trow[JJ] = (k == JJ) ? R.tau : col.trow[JJ];  // T[JJ][JJ] = tau_JJ
+  col.trow[JJ] = is_jj ? R.tau : col.trow[JJ];  // T[JJ][JJ] = tau_JJ
   col.prev_tau = R.tau;
 }
 
 template <int S, bool kVec>
 // At least two waves per SIMD (<= 256 VGPRs): 2048 matrices fill every SIMD
 // twice, and the second wave hides the first one's per-column latency.
-__global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
+__global__ __launch_bounds__(64 * kSnWaves, 2)
+__attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
     const float* __restrict__ A, int64_t sAb, int64_t sAr, int64_t sAc, float* __restrict__ H,
     float* __restrict__ tau, int batch, int n) {
   __shared__ __align__(16) SmallnShared<S> shm[kSnWaves];
@@ -317,6 +331,7 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_e
   const int k0 = lane & 15, g0 = lane >> 4;
   const int k = k0, g = g0;
   const float* Ab = A + (int64_t)b * sAb;
+  float* zrow = &sh.zb[0][k0];
 
   float c[S][4 * S];
   // kVec: n = 16 S, unit column stride, 16-byte aligned rows. Each load
@@ -395,8 +410,9 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_e
   static_for<0, S>([&](auto PI) {
     constexpr int p = decltype(PI)::value;
     constexpr int NT = S - p;  // row tiles at or below the panel's diagonal tile
-    const int kw = min(16, n - 16 * p);  // >= 1: S = ceil(n / 16)
-    const bool kin = k0 < kw;            // this lane's column exists
+    const int kw = kVec ? 16 : min(16, n - 16 * p);  // >= 1: S = ceil(n / 16)
+    // Lanes whose column exists (wave-uniform mask).
+    const uint64_t kin_mask = kVec ? ~uint64_t(0) : __builtin_amdgcn_ballot_w64(k0 < kw);
 
     // The steps only modify the panel's own rows >= 16 p: keep a copy for the
     // safe re-run (conflict-free b128 stores, lane-consecutive).
@@ -409,7 +425,7 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_e
     int bad = 0;
     static_for<0, 16>([&](auto JI) {
       constexpr int jj = decltype(JI)::value;
-      if (jj < kw) smalln_step<S, p, jj, false, kVec>(c, sh, k0, g0, n, kin, bad, col);
+      if (jj < kw) smalln_step<S, p, jj, false, kVec>(c, sh, zrow, n, kin_mask, bad, col);
     });
     if (__builtin_amdgcn_readfirstlane(bad)) [[unlikely]] {
       wave_lds_sync();
@@ -423,13 +439,13 @@ __global__ __launch_bounds__(64 * kSnWaves, 2) __attribute__((amdgpu_waves_per_e
       int unused = 0;
       static_for<0, 16>([&](auto JI) {
         constexpr int jj = decltype(JI)::value;
-        if (jj < kw) smalln_step<S, p, jj, true>(c, sh, k0, g0, n, kin, unused, col);
+        if (jj < kw) smalln_step<S, p, jj, true>(c, sh, zrow, n, kin_mask, unused, col);
       });
     }
     // The last column of T (the steps compute each column one step late).
     static_for<0, 16>([&](auto JI) {
       constexpr int jq = decltype(JI)::value;
-      if (jq == kw - 1) smalln_t_column<S, jq>(col, sh, k0);
+      if (jq == kw - 1) smalln_t_column<S, jq>(col, sh);
     });
     const float my_beta = col.beta, my_gamma = col.gamma, my_pre = col.pre, my_tau = col.tau;
 
