@@ -339,6 +339,31 @@ __device__ __forceinline__ bool lane_in(uint64_t mask) {
   return __builtin_amdgcn_inverse_ballot_w64(mask);
 }
 
+// rows16_sum(s) and rows16_bcast<GJ>(x) sharing their swaps: x is masked to
+// row group GJ and rides in the other half of the first permlane16_swap, so
+// the pairs (s, x) are summed side by side. Every lane ends with
+// sum = (s0 + s1) + (s2 + s3) and bcast = x of row group GJ (the other groups
+// add zeros). part holds sum in row groups 0 and 2 one swap earlier.
+template <int GJ>
+__device__ __forceinline__ void rows16_sum_bcast(float s, float x, float& sum, float& bcast,
+                                                 float& part) {
+  static_assert(GJ >= 0 && GJ < 4, "row group");
+  const float xm = lane_in(lanes_g_eq(GJ)) ? x : 0.0f;
+  // [s0, x0, s2, x2] and [s1, x1, s3, x3]
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(xm), false,
+                                                  false);
+  const float c = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  // [c0, c1, c0, c1] and [c2, c3, c2, c3]
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false,
+                                                  false);
+  const float d = __uint_as_float(b[0]) + __uint_as_float(b[1]);  // [S, X, S, X]
+  part = d;
+  const auto e = __builtin_amdgcn_permlane16_swap(__float_as_uint(d), __float_as_uint(d), false,
+                                                  false);
+  sum = __uint_as_float(e[0]);    // [S, S, S, S]
+  bcast = __uint_as_float(e[1]);  // [X, X, X, X]
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F&& f) {

@@ -26,9 +26,6 @@
 namespace qr {
 
 constexpr int kSnWaves = 4;     // matrices (one per wave) per workgroup
-#ifndef QR_SMALLN_SIGMA_FROM_DS
-#define QR_SMALLN_SIGMA_FROM_DS 1
-#endif
 constexpr int kSnVStride = 20;  // row stride of the V transpose buffer (floats)
 // Wait states before each fused-DPP asm block of the column steps: 1 (two
 // wait states) is what a DPP source written by the previous VALU instruction
@@ -41,6 +38,7 @@ struct SmallnShared {
   float vt[S * 16 * kSnVStride];  // V tiles of the current panel, row-major
   float zb[16][16];               // z_j = V[:, 0:j]^T v_j of the current panel
   float tb[16][17];               // T of the current panel
+  float refl[16][2];              // -beta and tau of the panel's columns
   // The panel's registers for the safe re-run; also the 16 x (16 S + 4) staging
   // tile of the vectorised load.
   float save[(S * 4 * 64) > 16 * (16 * S + 4) ? (S * 4 * 64) : 16 * (16 * S + 4)];
@@ -83,9 +81,10 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Per-panel reflector state of this lane's column (column 16 P + k), and row k
-// of the panel's compact-WY factor T (16 x 16, upper triangular).
+// of the panel's compact-WY factor T (16 x 16, upper triangular). beta and tau,
+// needed only when the panel is packed, wait in SmallnShared::refl.
 struct SmallnCol {
-  float beta = 0.0f, gamma = 1.0f, pre = 1.0f, tau = 0.0f;
+  float gamma = 1.0f, pre = 1.0f;
   float prev_tau = 0.0f;  // tau of the previous column step
   float trow[16] = {};
 };
@@ -224,14 +223,10 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   // run beside them.
   const float dsum = (dv[0] + dv[1]) + (dv[2] + dv[3]);
   const float alpha = readlane_f(c[P][4 * P + vj], JJ + 16 * gj);
-  const float ds = rows16_sum(dsum);
-  const float e = rows16_bcast<gj>(c[P][4 * P + vj]);  // row j of this column
-#if QR_SMALLN_SIGMA_FROM_DS
-  const float sigma = readlane_f(ds, JJ);  // lane JJ's dot is x^T x
-#else
-  const float sigma = (readlane_f(dsum, JJ) + readlane_f(dsum, JJ + 32)) +
-                      (readlane_f(dsum, JJ + 16) + readlane_f(dsum, JJ + 48));
-#endif
+  // ds = x^T c_k summed over the row groups, e = row j of this column.
+  float ds, e, dpart;
+  rows16_sum_bcast<gj>(dsum, c[P][4 * P + vj], ds, e, dpart);
+  const float sigma = readlane_f(dpart, JJ);  // lane JJ's dot is x^T x
   // No rows below the diagonal (the last column): tau = 0. With n = 16 S
   // known (kFullN) that is a compile-time fact, which saves the selects of
   // a runtime test in every step (cfg 2: 44.8 -> 43.0 us).
@@ -305,12 +300,10 @@ __device__ __forceinline__ void smalln_step(float (&c)[S][4 * S], SmallnShared<S
   // group stores the same value.
   // (Entries k >= JJ are never read.)
   zrow[16 * JJ] = (wk * col.pre) * col.gamma;
-  if (is_jj) {
-    col.beta = R.beta;
-    col.gamma = R.gamma;
-    col.pre = R.pre;
-    col.tau = R.tau;
-  }
+  // -beta and tau are wave-uniform: every lane stores the same pair.
+  *reinterpret_cast<float2*>(&sh.refl[JJ][0]) = float2{-R.beta, R.tau};
+  col.gamma = is_jj ? R.gamma : col.gamma;
+  col.pre = is_jj ? R.pre : col.pre;
   col.trow[JJ] = is_jj ? R.tau : col.trow[JJ];  // T[JJ][JJ] = tau_JJ
   col.prev_tau = R.tau;
 }
@@ -447,9 +440,12 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
       constexpr int jq = decltype(JI)::value;
       if (jq == kw - 1) smalln_t_column<S, jq>(col, sh);
     });
-    const float my_beta = col.beta, my_gamma = col.gamma, my_pre = col.pre, my_tau = col.tau;
+    const float2 rf = *reinterpret_cast<const float2*>(&sh.refl[k][0]);
+    const bool kin = k < kw;
+    const float my_beta = kin ? -rf.x : 0.0f, my_tau = kin ? rf.y : 0.0f;
+    const float my_gamma = col.gamma, my_pre = col.pre;
 
-    if (g == 0 && k < kw) tau[(int64_t)b * n + 16 * p + k] = my_tau;
+    if (g == 0 && kin) tau[(int64_t)b * n + 16 * p + k] = my_tau;
 
     // Final packing of the panel: R above the diagonal, beta on it, the
     // essential reflector v = (x pre) gamma below it.
