@@ -70,40 +70,66 @@ __device__ __forceinline__ float panel_dot_sum(const float* __restrict__ rp) {
   return (a4[0] + a4[1]) + (a4[2] + a4[3]);
 }
 
+// Sum of the NW per-wave partials at rp, in a fixed pairwise order (the same
+// in every lane of a column).
+template <int NW>
+__device__ __forceinline__ float panel_wave_sum(const float* __restrict__ rp) {
+  static_assert(NW % 4 == 0, "b128 reads of the partials");
+  f32x4 a4 = *reinterpret_cast<const f32x4*>(rp);
+#pragma unroll
+  for (int u = 1; u < NW / 4; ++u) {
+    const f32x4 q4 = *reinterpret_cast<const f32x4*>(rp + 4 * u);
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) a4[e4] += q4[e4];
+  }
+  return (a4[0] + a4[1]) + (a4[2] + a4[3]);
+}
+
 // Fast pass over the kw column steps of the panel whose diagonal rows
 // 16p..16p+15 are tile 0 of wave p. The steps are unrolled, and x (column J
 // below the diagonal) is read straight from the registers of lane J of each
 // 16-lane row by DPP row_newbcast, folded into the v_fmac of the dot and of
-// the update: no LDS traffic for x and one workgroup barrier per step.
+// the update: no LDS traffic for x and one workgroup barrier per step. Each
+// wave sums its four row groups with permlane swaps first, so the barrier
+// exchanges one partial per wave and column. Lane conditions are
+// compile-time lane masks (lanes_*), combined with wave-uniform ones: selects
+// on them read an SGPR pair instead of comparing per lane.
 // Returns false, with c and st meaningless, if some column was outside the
 // fast reflector's range (zero, tiny or huge norm); the result is then to be
 // recomputed by panel_general_pass.
 template <int NW, int RL>
 __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, RL>& sh, int p,
                                                 int r, int kw, int w, int lane, PanelCol& st) {
-  using S = Strip<NW, RL>;
-  const int k = lane & 15, g = lane >> 4;
+  const int k = lane & 15;
   const int d0 = 16 * p;
+  // Lanes whose column exists; tile 0 of wave w lies wholly below the panel's
+  // diagonal rows (w > p), above them (w < p), or is the diagonal tile (w = p).
+  const uint64_t kin = __builtin_amdgcn_ballot_w64(k < kw);
+  const bool diag = w == p;
+  const uint64_t tile0_rows = w > p ? ~uint64_t(0) : uint64_t(0);
   int bad = 0;  // wave-uniform integer flag (a bool becomes a per-lane 0/1 here)
   static_for<0, 16>([&](auto jc) __attribute__((always_inline)) {
     constexpr int J = decltype(jc)::value;
     if (J >= kw) return;
     const int dj = d0 + J;
-    if (w == p && g == (J >> 2)) sh.erow[J & 1][k] = c[J & 3];
-    // Rows <= dj (where x is zero) all lie in tile 0.
-    float dv[4];
+    constexpr uint64_t row_j = lanes_g_eq(J >> 2);  // row group of row dj in tile 0
+    if (lane_in(diag ? row_j : 0)) sh.erow[J & 1][k] = c[J & 3];
+    // Tile 0's broadcast with its rows <= dj zeroed, kept for the update.
+    float xb0[4], dv[4];
+    static_for<0, 4>([&](auto vc) __attribute__((always_inline)) {
+      constexpr int v = decltype(vc)::value;
+      constexpr uint64_t below = lanes_g_ge((J - v + 4) / 4);  // 4 g + v > J
+      xb0[v] = lane_in(diag ? below : tile0_rows) ? row_bcast16<J>(c[v]) : 0.0f;
+      dv[v] = xb0[v] * c[v];
+    });
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float xb = row_bcast16<J>(c[v]);
-      dv[v] = ((S::row(0, v, w, g) > dj) ? xb : 0.0f) * c[v];
-    }
-#pragma unroll
-    for (int t = 1; t < S::kTiles; ++t)
+    for (int t = 1; t < RL / 4; ++t)
       dot4_bcast16<J>(dv[0], dv[1], dv[2], dv[3], c[4 * t], c[4 * t + 1], c[4 * t + 2],
                       c[4 * t + 3]);
-    sh.red[J & 1][k][4 * w + g] = (dv[0] + dv[1]) + (dv[2] + dv[3]);
+    const float dw = rows16_sum((dv[0] + dv[1]) + (dv[2] + dv[3]));
+    if (lane_in(lanes_g_eq(0))) sh.red[J & 1][k][w] = dw;
     __syncthreads();
-    const float ds = panel_dot_sum<NW>(sh.red[J & 1][k]);
+    const float ds = panel_wave_sum<NW>(&sh.red[J & 1][k][0]);
     const float e = sh.erow[J & 1][k];
     const float sigma = readlane_f(ds, J);
     const float alpha = readlane_f(e, J);
@@ -113,26 +139,23 @@ __device__ __forceinline__ bool panel_fast_pass(float (&c)[RL], PanelShared<NW, 
     if (ident) R = reflector_identity(alpha);
     const float wk = fmaf(R.gamma, ds, e);  // v_J^T c_k
     const float cc = R.tau * wk;
-    const bool upd = (k > J) && (k < kw);
-    const float ncx = upd ? -(cc * R.gamma) : 0.0f;
+    const float ncx = lane_in(lanes_k_gt(J) & kin) ? -(cc * R.gamma) : 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float xb = row_bcast16<J>(c[v]);
-      c[v] = fmaf(ncx, (S::row(0, v, w, g) > dj) ? xb : 0.0f, c[v]);
-    }
+    for (int v = 0; v < 4; ++v) c[v] = fmaf(ncx, xb0[v], c[v]);
 #pragma unroll
-    for (int t = 1; t < S::kTiles; ++t)
+    for (int t = 1; t < RL / 4; ++t)
       axpy4_bcast16<J>(c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3], ncx);
-    if (upd && w == p && g == (J >> 2)) c[J & 3] -= cc;  // v_J[dj] = 1
+    // v_J[dj] = 1
+    const float cj = c[J & 3] - cc;
+    c[J & 3] = lane_in(diag ? lanes_k_gt(J) & kin & row_j : 0) ? cj : c[J & 3];
     // Column J of T needs z_k = V_k^T v_J = (c_k[dj] + gamma x^T c_k) gamma_k, k < J.
-    if (w == 0 && g == 0 && k < J) sh.zbuf[J][k] = wk * st.gamma;
-    if (k == J) {
-      st.beta = R.beta;
-      st.gamma = R.gamma;
-      st.pre = 1.0f;
-      st.tau = R.tau;
-    }
+    if (lane_in(w == 0 ? lanes_g_eq(0) & lanes_k_lt(J) : 0)) sh.zbuf[J][k] = wk * st.gamma;
+    const bool own = lane_in(lanes_k_eq(J));
+    st.beta = own ? R.beta : st.beta;
+    st.gamma = own ? R.gamma : st.gamma;
+    st.tau = own ? R.tau : st.tau;
   });
+  st.pre = 1.0f;
   return __builtin_amdgcn_readfirstlane(bad) == 0;
 }
 

@@ -323,6 +323,12 @@ constexpr uint64_t lanes_k_eq(int j) {
     if ((l & 15) == j) m |= uint64_t(1) << l;
   return m;
 }
+constexpr uint64_t lanes_k_lt(int j) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l)
+    if ((l & 15) < j) m |= uint64_t(1) << l;
+  return m;
+}
 constexpr uint64_t lanes_g_eq(int g) {
   uint64_t m = 0;
   for (int l = 0; l < 64; ++l)
