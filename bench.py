@@ -59,13 +59,13 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 # profile_run runs first (FETCH x2.000, WRITE x1.000). Counters cannot be read
 # from inside this process; rerun those commands after changing a kernel.
 HBM_MIB_PER_CALL = {
-    "smalln": {2: 32.9 + 32.8},
+    "smalln": {2: 32.7 + 46.8},
     # k_panel + k_panel_seq (fallback panels of the CholeskyQR2 route), both
     # traced as "panel".
-    "panel": {3: 1150.1 + 298.6, 4: 23.3 + 6.8, 5: 13.9 + 5.2},
-    "trail": {3: 2488.6 + 1698.1, 4: 1806.9 + 1433.4, 5: 3254.9 + 2809.5},
+    "panel": {3: 1146.7 + 298.6, 4: 4.9 + 1.3, 5: 7.4 + 3.9},
+    "trail": {3: 2489.2 + 1697.5, 4: 1803.8 + 1433.8, 5: 3254.8 + 2807.0},
     # k_cq_gram + k_cq_chol1 + k_cq_recon + k_cq_form of the CholeskyQR2 route.
-    "cholqr": {3: 194.9 + 119.0, 4: 361.1 + 200.1, 5: 379.7 + 193.3},
+    "cholqr": {3: 194.8 + 118.9, 4: 379.5 + 213.5, 5: 383.1 + 196.6},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
