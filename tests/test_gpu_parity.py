@@ -65,6 +65,26 @@ def test_fused_smalln_vs_oracle(oracle, n, batch):
     assert np.all(tau[:, -1] == 0.0)
 
 
+@pytest.mark.parametrize("n", [64, 40])
+@pytest.mark.parametrize("scale", [1e-30, 1e25, 1e-40, 0.0], ids=["tiny", "huge", "denormal", "zero"])
+def test_fused_smalln_extreme_columns_vs_oracle(oracle, n, scale):
+    """A column outside the fast reflector's range in every panel (matrix k has
+    it in column 16 k + 5 of its panel k, one column per matrix): each panel's
+    fast pass hands over to the out-of-line safe re-run of that panel, for the
+    vectorised n = 64 kernel and the general one."""
+    _say(f"fused_smalln extreme columns n={n} scale={scale:g}")
+    A = _gauss(5, n, seed=n + 11)
+    for b in range(4):
+        col = 16 * b + 5
+        if col < n:
+            A[b, :, col] *= scale
+    H, tau = hip_qr.fused_smalln(A.to(DEV))
+    torch.cuda.synchronize()
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
+                  what=f"smalln extreme n={n} scale={scale:g}")
+
+
 def test_fused_smalln_strided_input(oracle):
     _say("fused_smalln strided (transposed) input n=40")
     A = _gauss(3, 40, seed=7)
