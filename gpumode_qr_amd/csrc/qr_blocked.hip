@@ -400,8 +400,16 @@ __device__ __forceinline__ void panel_factor(PanelShared<NW, RL>& sh, int b, flo
 // null: the first outer block reads the caller's matrix directly. When `only`
 // is not null, only matrices b with only[b] == 1 are factored (the others
 // return at once).
+// Panels of 4 or 8 waves and up to 16 strip registers run at most 80 VGPRs
+// (six waves per SIMD), so that three 8-wave or six 4-wave workgroups share a
+// CU: at b640 n512 the 640 panels of a launch run in one round instead of two.
+// Wider strips keep their registers.
 template <int NW, int RL>
-__global__ __launch_bounds__(64 * NW) void k_panel(float* __restrict__ H, int64_t sHb,
+constexpr int kPanelWavesPerEu = (NW <= 8 && RL <= 16) ? 6 : 1;
+
+template <int NW, int RL>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(kPanelWavesPerEu<NW, RL>))) void k_panel(float* __restrict__ H, int64_t sHb,
                                                    int64_t ldh, int J0, int p, int r, int kw,
                                                    float* __restrict__ tau, int64_t sTaub,
                                                    float* __restrict__ Tws, int64_t sTwb,

@@ -34,8 +34,10 @@ struct Strip {
 constexpr int kVStride = 20;
 
 // 16-row tiles of V staged per wave at a time (LDS budget: NW * tiles * 1.25 KB).
+// Two at 8 waves: the 512-row panel kernel then needs 38 KB of LDS, so three of
+// its workgroups share a CU (the 16-wave kernels stage four).
 #ifndef QR_STAGE_TILES_MAX
-#define QR_STAGE_TILES_MAX 8
+#define QR_STAGE_TILES_MAX 2
 #endif
 template <int NW, int RL>
 struct StageTiles {
