@@ -77,14 +77,14 @@ size_t ws_t_bytes(int batch) { return align_up((size_t)batch * kTStride * sizeof
 size_t ws_cq_bytes(int batch) { return align_up(qr::cq_workspace_floats(batch) * sizeof(float)); }
 
 // Outer blocks of 64 columns with at least this many rows take the CholeskyQR2
-// route: 128 rows in calls of at most 64 matrices, 512 above (with many
+// route: 128 rows in calls of at most 64 matrices, 576 above (with many
 // matrices the Householder panels of short blocks are throughput-bound and
 // cheaper). opts->cholqr = 0 switches the route off; opts->cholqr_min_rows
 // sets the bound (the route needs r > 64).
 int cq_min_rows(int batch, const qr_options& o) {
   if (!o.cholqr) return 1 << 30;
   if (o.cholqr_min_rows) return o.cholqr_min_rows;
-  return batch <= 64 ? 128 : 512;
+  return batch <= 64 ? 128 : 576;
 }
 
 // Panels per outer block (opts->outer_panels, 0 = 4).

@@ -58,7 +58,7 @@ size_t qr_geqrf_f32_workspace(int batch, int n);
  * Full factorisation, replacing the champion variant's forward pass
  * (reference src/qrbench/variants.py:876-917 -> :761-805 for n > 128 and
  * :698-758 for n <= 128; baseline torch.geqrf at src/qrbench/reference.py:18-20).
- * Outer blocks of >= 128 rows (calls of at most 64 matrices; >= 512 rows above)
+ * Outer blocks of >= 128 rows (calls of at most 64 matrices; >= 576 rows above)
  * are factored by CholeskyQR2 with Householder reconstruction (the CholeskyQR
  * route of references/nvidia_winner_sol_combo.md:1051-1052), with the same
  * (V, tau, R) output; matrices it cannot factor to that standard take the
@@ -86,7 +86,7 @@ int qr_geqrf_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H
 typedef struct qr_options {
   int cholqr;          /* 1 (default): 64-column outer blocks of >= cholqr_min_rows rows take
                           the CholeskyQR2 route; 0: Householder panels for every block */
-  int cholqr_min_rows; /* 0 (default): 128 rows in calls of <= 64 matrices, 512 above;
+  int cholqr_min_rows; /* 0 (default): 128 rows in calls of <= 64 matrices, 576 above;
                           else the row bound itself (>= 65) */
   int cholqr_one_pass; /* 1 (default): one CholeskyQR pass where ||R1s^-1||_F^2 <= 144,
                           else two; 0: always two; 2: one pass only, a matrix that would

@@ -351,18 +351,21 @@ def test_config5_gates_and_gaussian_half_parity(oracle):
                   what="cfg5 Gaussian half")
 
 
-def test_config3_full_batch_gates_and_sampled_parity(oracle):
-    """All 640 matrices through the default route, as the benchmark runs them
-    (more than 64 matrices: the CholeskyQR2 route on the first, 512-row block
-    only, then the 4-wave panels and the b640 trailing-update shapes). Gates on
-    the whole batch, oracle parity on five matrices spread over it."""
-    _say("config 3 (b640 n512), full batch")
+@pytest.mark.parametrize("route", [False, True], ids=["default", "route512"])
+def test_config3_full_batch_gates_and_sampled_parity(oracle, route):
+    """All 640 matrices as the benchmark runs them (more than 64 matrices: by
+    default every block takes the 4-wave Householder panels and the b640
+    trailing-update shapes), and with the CholeskyQR2 route on the first,
+    512-row block (cholqr_min_rows=512). Gates on the whole batch, oracle
+    parity on five matrices spread over it."""
+    _say(f"config 3 (b640 n512), full batch, route={route}")
     A = inputs.config_tensor(inputs.config_spec(3))
-    H, tau, codes = _run_ws(A)
+    H, tau, codes = _run_ws(A, **({"cholqr_min_rows": 512} if route else {}))
     assert torch.isfinite(H).all() and torch.isfinite(tau).all()
     res = checker.check(A, H, tau)
     assert res.passed, res.as_dict()
-    assert bool((codes != 1).all())  # no matrix left the route in its block
+    if route:
+        assert bool((codes != 1).all())  # no matrix left the route in its block
     idx = [0, 157, 320, 481, 639]
     H_ref, tau_ref = oracle.geqrf(A[idx].numpy(), nb=16)
     assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref,
@@ -624,7 +627,7 @@ def test_run_baseline_db_record_schema(tmp_path):
 # --------------------------------------------------------------------------
 # Outer blocks by CholeskyQR2 + Householder reconstruction (qr_cholqr.hip).
 # cholqr_min_rows=65 sends every full 64-column block through the route (by
-# default blocks of >= 128 rows in calls of <= 64 matrices, >= 512 above);
+# default blocks of >= 128 rows in calls of <= 64 matrices, >= 576 above);
 # cholqr=0 switches it off. Route codes of the last route block: 0 two
 # passes, 1 Householder panels (guard failed), 2 one pass.
 
