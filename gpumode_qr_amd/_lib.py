@@ -26,6 +26,7 @@ class Options(ctypes.Structure):
         ("cholqr_fused", ctypes.c_int),
         ("lookahead", ctypes.c_int),
         ("outer_panels", ctypes.c_int),
+        ("midn", ctypes.c_int),
     ]
 
     def as_dict(self) -> dict:
@@ -94,7 +95,7 @@ SIGNATURES: dict[str, tuple] = {
 # qr_kernel_id values of include/qr_gfx950.h
 KERNELS = {"smalln": 0, "panel": 1, "trail": 2, "copy": 3, "larft": 4, "apply": 5, "cholqr": 6}
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 QR_OK = 0
 

@@ -22,7 +22,7 @@ LIB = PKG / "libqr_gfx950.so"
 ARCH = "gfx950"
 
 SOURCES = [
-    "qr_smalln.hip", "qr_blocked.hip", "qr_cholqr.hip", "qr_apply.hip", "qr_larft.hip",
+    "qr_smalln.hip", "qr_midn.hip", "qr_blocked.hip", "qr_cholqr.hip", "qr_apply.hip", "qr_larft.hip",
     "qr_copy.hip", "qr_api.hip",
 ]
 

@@ -22,6 +22,9 @@
 namespace qr {
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                                float* tau, int batch, int n, hipStream_t stream);
+hipError_t launch_geqrf_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                             float* tau, int batch, int n, hipStream_t stream);
+int midn_max_n();
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
                         float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
                         int64_t sAb, int64_t lda, int batch, hipStream_t stream,
@@ -58,7 +61,7 @@ hipError_t launch_eye(float* Q, int64_t sQb, int64_t ldq, int batch, int n, hipS
 
 namespace {
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 constexpr int kMaxN = 4096;
 constexpr int kSmallN = 64;
 constexpr int kPanel = 16;
@@ -95,10 +98,22 @@ bool options_valid(const qr_options& o) {
          (o.cholqr_min_rows == 0 || (o.cholqr_min_rows >= 65 && o.cholqr_min_rows <= kMaxN)) &&
          (o.cholqr_one_pass >= 0 && o.cholqr_one_pass <= 2) &&
          (o.cholqr_fused == 0 || o.cholqr_fused == 1) && (o.lookahead == 0 || o.lookahead == 1) &&
-         o.outer_panels >= 0 && o.outer_panels <= kMaxBlocks;
+         o.outer_panels >= 0 && o.outer_panels <= kMaxBlocks && o.midn >= 0 && o.midn <= 2;
 }
 
-constexpr qr_options kDefaultOptions = {1, 0, 1, 0, 1, 0};
+constexpr qr_options kDefaultOptions = {1, 0, 1, 0, 1, 0, 1};
+
+// 64 < n <= 192 in one launch of the fused mid-n kernel (one workgroup per
+// matrix) up to batch * ceil(n / 16) = 8192 waves of work: measured against
+// the blocked route, 0.5-0.65x its time up to 128 matrices at n = 80..192 and
+// 0.86-0.93x at 512; at 2048 matrices 0.88x for n = 80, 0.97x for n = 128 and
+// 1.3x for n = 176-192 (a workgroup per matrix holds a CU longer than the
+// blocked route's throughput-bound panels).
+constexpr int64_t kMidnMaxWaves = 8192;
+bool midn_route(int batch, int n, const qr_options& o) {
+  if (o.midn == 0 || n <= kSmallN || n > qr::midn_max_n()) return false;
+  return o.midn == 2 || (int64_t)batch * ((n + 15) / 16) <= kMidnMaxWaves;
+}
 
 int to_status(hipError_t e) { return e == hipSuccess ? QR_OK : QR_ELAUNCH; }
 
@@ -197,6 +212,17 @@ hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, flo
   const double bytes = (2.0 * n * n + n) * 4.0 * batch;
   return traced(QR_KERNEL_SMALLN, flops, bytes, s, [&] {
     return qr::launch_geqrf_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s);
+  });
+}
+
+// The fused mid-n kernel (64 < n <= 192, one workgroup per matrix), traced with
+// the small-n kernel as the fused whole-matrix family.
+hipError_t run_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
+                    int batch, int n, hipStream_t s) {
+  const double flops = 4.0 / 3.0 * n * n * (double)n * batch;
+  const double bytes = (2.0 * n * n + n) * 4.0 * batch;
+  return traced(QR_KERNEL_SMALLN, flops, bytes, s, [&] {
+    return qr::launch_geqrf_midn(A, sAb, sAr, sAc, H, tau, batch, n, s);
   });
 }
 
@@ -325,8 +351,10 @@ int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, f
                         float* tau, int batch, int n, void* stream) {
   int st = check_geqrf_args(A, sAb, sAr, sAc, H, tau, batch, n);
   if (st != QR_OK || batch == 0 || n == 0) return st;
-  if (n > kSmallN) return QR_EUNSUPPORTED;
-  return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, static_cast<hipStream_t>(stream)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n <= kSmallN) return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s));
+  if (n <= qr::midn_max_n()) return to_status(run_midn(A, sAb, sAr, sAc, H, tau, batch, n, s));
+  return QR_EUNSUPPORTED;
 }
 
 void qr_default_options(qr_options* opts) {
@@ -357,6 +385,7 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
 
   const size_t need = qr_geqrf_f32_workspace(batch, n);
   if (workspace_bytes < need || !workspace) return QR_EWORKSPACE;
+  if (midn_route(batch, n, o)) return to_status(run_midn(A, sAb, sAr, sAc, H, tau, batch, n, s));
   // Two T slots per matrix: outer block k uses slot k & 1, so the panels of
   // block k+1 never overwrite T factors that block k's trailing update reads.
   float* Tslot[2] = {static_cast<float*>(workspace),

@@ -125,7 +125,8 @@ def route_codes(workspace: torch.Tensor, batch: int, n: int) -> torch.Tensor:
 
 
 def fused_smalln(A: torch.Tensor):
-    """Kernel (a) alone: n <= 64, one wavefront per matrix."""
+    """Kernel (a) alone, one launch: n <= 64 one wavefront per matrix,
+    64 < n <= 192 one workgroup per matrix (a wavefront per 16-column strip)."""
     _check_input(A)
     lib = _lib.load()
     b, n, _ = A.shape

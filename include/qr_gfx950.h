@@ -97,6 +97,9 @@ typedef struct qr_options {
   int lookahead;       /* 1 (default): rest of the trailing update on a second stream */
   int outer_panels;    /* 16-wide panels per outer block, 1..8; 0 (default): 4. The
                           CholeskyQR2 route needs 4. */
+  int midn;            /* 64 < n <= 192: 1 (default) the one-launch fused kernel when
+                          batch * ceil(n / 16) <= 8192, else the blocked route; 0: always
+                          the blocked route; 2: always the fused kernel */
 } qr_options;
 
 /* Fills *opts with the defaults qr_geqrf_f32 runs with. */
@@ -140,9 +143,13 @@ int qr_geqrf_f32_noalloc(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, 
                          float* tau, int batch, int n, void* stream);
 
 /*
- * Kernel (a): fused small-n factorisation, n <= 64, one wavefront per matrix.
+ * Kernel (a): fused whole-matrix factorisation in one launch, n <= 192: one
+ * wavefront per matrix for n <= 64; one workgroup per matrix (a wavefront per
+ * 16-column strip, the matrix held in registers) for 64 < n <= 192.
  * Replaces hh_fused_qr / _hh_fused_qr_kernel (reference
- * src/qrbench/triton_kernels.py:641-755). Same arguments as qr_geqrf_f32.
+ * src/qrbench/triton_kernels.py:641-755) and the fused route of
+ * make_hh_fused_smalln (src/qrbench/variants.py:739-758, n <= 128). Same
+ * arguments as qr_geqrf_f32; QR_EUNSUPPORTED above n = 192.
  */
 int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                         float* tau, int batch, int n, void* stream);

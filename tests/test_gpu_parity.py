@@ -85,6 +85,85 @@ def test_fused_smalln_extreme_columns_vs_oracle(oracle, n, scale):
                   what=f"smalln extreme n={n} scale={scale:g}")
 
 
+@pytest.mark.parametrize("n", [65, 80, 96, 100, 128, 144, 176, 192])
+def test_fused_midn_vs_oracle(oracle, n):
+    """64 < n <= 192 in one launch: a workgroup per matrix, a wave per strip."""
+    _say(f"fused mid-n n={n} batch=3")
+    A = _gauss(3, n, seed=300 + n)
+    H, tau = hip_qr.fused_smalln(A.to(DEV))
+    torch.cuda.synchronize()
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
+                  what=f"midn n={n}")
+    assert np.all(tau.cpu().numpy()[:, -1] == 0.0)
+
+
+@pytest.mark.parametrize("n", [128, 100])
+@pytest.mark.parametrize("scale", [1e-30, 1e25, 1e-40, 0.0], ids=["tiny", "huge", "denormal", "zero"])
+def test_fused_midn_extreme_columns_vs_oracle(oracle, n, scale):
+    """A column outside the fast reflector's range in a panel of each matrix
+    (matrix b: column 16 b + 5 of panel b, last matrix: the last panel's first
+    column): the panel's fast pass hands over to the rolled safe path."""
+    _say(f"fused mid-n extreme columns n={n} scale={scale:g}")
+    nr = (n + 15) // 16
+    A = _gauss(nr, n, seed=n + 17)
+    for b in range(nr):
+        col = min(16 * b + 5, n - 1) if b < nr - 1 else 16 * (nr - 1)
+        A[b, :, col] *= scale
+    H, tau = hip_qr.fused_smalln(A.to(DEV))
+    torch.cuda.synchronize()
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
+                  what=f"midn extreme n={n} scale={scale:g}")
+
+
+def test_fused_midn_strided_input(oracle):
+    _say("fused mid-n strided (transposed) input n=150")
+    A = _gauss(2, 150, seed=8)
+    At = A.transpose(1, 2).contiguous().transpose(1, 2)  # same values, column-major
+    H, tau = hip_qr.fused_smalln(At.to(DEV))
+    torch.cuda.synchronize()
+    H_ref, tau_ref = oracle.geqrf(A.numpy())
+    assert_parity(A.numpy(), H.cpu().numpy(), tau.cpu().numpy(), H_ref, tau_ref,
+                  what="midn strided n=150")
+
+
+@pytest.mark.parametrize("n,batch,fused", [(80, 3, True), (176, 40, True), (192, 682, True),
+                                           (192, 683, False), (176, 800, False)])
+def test_geqrf_mid_n_route_choice_bitwise(n, batch, fused):
+    """geqrf's default for 64 < n <= 192: the fused kernel up to batch *
+    ceil(n / 16) = 8192, the blocked route above; midn=2 / midn=0 force one or
+    the other. Each default result equals its forced route bit for bit."""
+    _say(f"mid-n route choice n={n} batch={batch} fused={fused}")
+    A = _gauss(batch, n, seed=n + batch).to(DEV)
+    H, tau = hip_qr.geqrf(A)
+    Hf, tf = hip_qr.geqrf(A, options=hip_qr.options(midn=2))
+    Hb, tb = hip_qr.geqrf(A, options=hip_qr.options(midn=0))
+    torch.cuda.synchronize()
+    Hx, tx = (Hf, tf) if fused else (Hb, tb)
+    assert torch.equal(H, Hx) and torch.equal(tau, tx)
+    assert not torch.equal(Hf, Hb)  # two different kernels: not the same bits
+    res = checker.check(A.cpu(), H.cpu(), tau.cpu())
+    assert res.passed, res.as_dict()
+
+
+def test_fused_midn_padded_input_bitwise(oracle):
+    """Unit column stride with padded rows and batch is read in place; the
+    column-major view of the same values gives the same bits."""
+    n = 100
+    _say(f"fused mid-n padded input (n={n})")
+    base = torch.randn(2, n + 3, n + 7, generator=torch.Generator().manual_seed(5))
+    Ap = base.to(DEV)[:, 1:n + 1, 2:n + 2]
+    Ac = Ap.transpose(1, 2).contiguous().transpose(1, 2)
+    Hp, tp = hip_qr.fused_smalln(Ap)
+    Hc, tc = hip_qr.fused_smalln(Ac)
+    torch.cuda.synchronize()
+    assert torch.equal(Hp, Hc) and torch.equal(tp, tc)
+    H_ref, tau_ref = oracle.geqrf(Ap.cpu().numpy())
+    assert_parity(Ap.cpu().numpy(), Hp.cpu().numpy(), tp.cpu().numpy(), H_ref, tau_ref,
+                  what="midn padded n=100")
+
+
 def test_fused_smalln_strided_input(oracle):
     _say("fused_smalln strided (transposed) input n=40")
     A = _gauss(3, 40, seed=7)
@@ -246,7 +325,7 @@ def test_wy_update_vs_oracle(oracle, r, nblk, c):
 def test_geqrf_blocked_vs_oracle(oracle, n):
     _say(f"geqrf blocked n={n}")
     A = _gauss(3, n, seed=n)
-    H, tau = _run(A)
+    H, tau = _run(A, midn=0)  # the blocked route also for n <= 192
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"n={n}")
     res = checker.check(A, H, tau)
@@ -395,7 +474,7 @@ def test_blocked_extreme_columns_vs_oracle(oracle, n, cols, scale):
     A[0, :, cols[0]] *= scale
     A[1, :, cols[1]] *= scale
     A[1, :, cols[2]] *= scale
-    H, tau = _run(A)
+    H, tau = _run(A, midn=0)
     assert torch.isfinite(H).all() and torch.isfinite(tau).all()
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"n={n} x{scale:g}")
@@ -469,7 +548,7 @@ def test_first_block_reads_padded_input_directly(n, lookahead):
     n + 7, batch stride (n + 3) (n + 7)) is read in place by the first outer
     block's kernels; a column-major view of the same values goes through the
     strided copy first. Both give the same bits, with and without look-ahead."""
-    opts = hip_qr.options(lookahead=int(lookahead))
+    opts = hip_qr.options(lookahead=int(lookahead), midn=0)
     _say(f"padded input read directly (n={n}, lookahead={lookahead})")
     batch = 2
     base = torch.randn(batch, n + 3, n + 7, generator=torch.Generator().manual_seed(n))
@@ -626,12 +705,13 @@ def test_run_baseline_db_record_schema(tmp_path):
 
 # --------------------------------------------------------------------------
 # Outer blocks by CholeskyQR2 + Householder reconstruction (qr_cholqr.hip).
-# cholqr_min_rows=65 sends every full 64-column block through the route (by
+# cholqr_min_rows=65 (with midn=0 for n <= 192) sends every full 64-column
+# block through the route (by
 # default blocks of >= 128 rows in calls of <= 64 matrices, >= 576 above);
 # cholqr=0 switches it off. Route codes of the last route block: 0 two
 # passes, 1 Householder panels (guard failed), 2 one pass.
 
-EVERY_BLOCK = {"cholqr_min_rows": 65}
+EVERY_BLOCK = {"cholqr_min_rows": 65, "midn": 0}
 
 
 @pytest.mark.parametrize("n", [128, 129, 200, 256, 300, 513, 1100])
@@ -692,7 +772,7 @@ def test_cholqr_one_pass_bound_vs_oracle(oracle, inv_sum, code):
     for b in range(2):
         blk, kappa = near_bound_block(n, inv_sum, seed=b)
         A[b, :, :64] = torch.from_numpy(blk)
-    H, tau, codes = _run_ws(A)
+    H, tau, codes = _run_ws(A, midn=0)
     print(f"[gpu-case] near-bound kappa(R1s) about {kappa:.1f}, codes {codes.tolist()}",
           flush=True)
     assert codes.tolist() == [code, code], codes
@@ -712,7 +792,7 @@ def test_cholqr_one_pass_only_sends_two_pass_blocks_to_the_panels(oracle):
     A = torch.randn(2, n, n, generator=g)
     blk, _ = near_bound_block(n, 152.0, seed=0)
     A[0, :, :64] = torch.from_numpy(blk)
-    H, tau, codes = _run_ws(A, cholqr_one_pass=2)
+    H, tau, codes = _run_ws(A, cholqr_one_pass=2, midn=0)
     assert codes.tolist() == [1, 2], codes
     H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what="one pass only")
@@ -771,7 +851,7 @@ def test_cholqr_fallback_route_codes(kind):
     _say(f"cholqr fallback route code {kind} n={n}")
     A = _gauss(3, n, seed=77)
     A[1, :, 30] = 0.0 if kind == "zero" else A[1, :, 30] * (1e-30 if kind == "tiny" else 1e-40)
-    _, _, codes = _run_ws(A)
+    _, _, codes = _run_ws(A, midn=0)
     assert codes.tolist() == [2, 1, 2], codes
 
 

@@ -78,7 +78,7 @@ def test_argument_validation_without_launch(lib):
     # workspace missing for the blocked route
     assert lib.qr_geqrf_f32(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, None) == 3
     # kernel-level entry points
-    assert lib.qr_fused_smalln_f32(p, 100 * 100, 100, 1, h, t, 1, 100, None) == 2
+    assert lib.qr_fused_smalln_f32(p, 200 * 200, 200, 1, h, t, 1, 200, None) == 2
     assert lib.qr_panel_f32(h, 100, 10, 0, 0, 10, 17, t, 17, t, 256, 1, None) == 1  # kw > 16
     assert lib.qr_panel_f32(h, 9000, 90, 0, 8, 200, 16, t, 90, t, 4096, 1, None) == 1  # p >= 8
     assert lib.qr_panel_f32(h, 9000, 90, 0, 2, 40, 16, t, 90, t, 512, 1, None) == 1  # r < 16p+kw
@@ -104,7 +104,7 @@ def test_argument_validation_without_launch(lib):
 def test_route_options_defaults_and_validation(lib):
     o = _lib.default_options()
     assert o.as_dict() == {"cholqr": 1, "cholqr_min_rows": 0, "cholqr_one_pass": 1,
-                           "cholqr_fused": 0, "lookahead": 1, "outer_panels": 0}
+                           "cholqr_fused": 0, "lookahead": 1, "outer_panels": 0, "midn": 1}
     p = ctypes.c_void_p(0x1000)
     h = ctypes.c_void_p(0x10000000)
     t = ctypes.c_void_p(0x20000000)
@@ -113,7 +113,7 @@ def test_route_options_defaults_and_validation(lib):
     for field, bad in (("cholqr", 2), ("cholqr_min_rows", 64), ("cholqr_min_rows", 5000),
                        ("cholqr_one_pass", -1), ("cholqr_one_pass", 3), ("cholqr_fused", 2),
                        ("lookahead", 7),
-                       ("outer_panels", 9), ("outer_panels", -1)):
+                       ("outer_panels", 9), ("outer_panels", -1), ("midn", 3), ("midn", -1)):
         o = _lib.default_options()
         setattr(o, field, bad)
         assert ex(p, 200 * 200, 200, 1, h, t, 1, 200, None, 0, ctypes.byref(o), None) == 1, field
