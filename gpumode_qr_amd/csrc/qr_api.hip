@@ -23,7 +23,8 @@ namespace qr {
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                                float* tau, int batch, int n, hipStream_t stream);
 hipError_t launch_geqrf_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
-                             float* tau, int batch, int n, hipStream_t stream);
+                             int64_t sHb, int64_t ldh, float* tau, int64_t sTaub, int batch,
+                             int n, hipStream_t stream);
 int midn_max_n();
 hipError_t launch_panel(float* H, int64_t sHb, int64_t ldh, int J0, int p, int r, int kw,
                         float* tau, int64_t sTaub, float* Tws, int64_t sTwb, const float* A,
@@ -109,10 +110,18 @@ constexpr qr_options kDefaultOptions = {1, 0, 1, 0, 1, 0, 1};
 // 0.86-0.93x at 512; at 2048 matrices 0.88x for n = 80, 0.97x for n = 128 and
 // 1.3x for n = 176-192 (a workgroup per matrix holds a CU longer than the
 // blocked route's throughput-bound panels).
+// The blocked route's last r <= 192 columns go to the same kernel, in place,
+// under a tighter bound of 2048: measured against the blocked tail (ms),
+// b40 n352 0.365 -> 0.327, b40 n200 0.193 -> 0.144, b60 n1024 2.229 -> 2.210,
+// b2 n4096 7.266 -> 7.243, but b300 n300 0.557 -> 0.569 and b640 n512
+// 2.493 -> 2.596 (there the blocked tail's panels overlap the previous
+// block's update on the second stream).
 constexpr int64_t kMidnMaxWaves = 8192;
-bool midn_route(int batch, int n, const qr_options& o) {
+constexpr int64_t kMidnTailMaxWaves = 2048;
+bool midn_route(int batch, int n, const qr_options& o, bool tail = false) {
   if (o.midn == 0 || n <= kSmallN || n > qr::midn_max_n()) return false;
-  return o.midn == 2 || (int64_t)batch * ((n + 15) / 16) <= kMidnMaxWaves;
+  return o.midn == 2 ||
+         (int64_t)batch * ((n + 15) / 16) <= (tail ? kMidnTailMaxWaves : kMidnMaxWaves);
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? QR_OK : QR_ELAUNCH; }
@@ -217,12 +226,15 @@ hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, flo
 
 // The fused mid-n kernel (64 < n <= 192, one workgroup per matrix), traced with
 // the small-n kernel as the fused whole-matrix family.
-hipError_t run_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
-                    int batch, int n, hipStream_t s) {
+// H and tau of (batch, n, n) and (batch, n) matrices at strides (sHb, ldh, 1)
+// and (sTaub, 1); A may be H itself (in-place factorisation of the blocked
+// route's last columns).
+hipError_t run_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, int64_t sHb,
+                    int64_t ldh, float* tau, int64_t sTaub, int batch, int n, hipStream_t s) {
   const double flops = 4.0 / 3.0 * n * n * (double)n * batch;
   const double bytes = (2.0 * n * n + n) * 4.0 * batch;
   return traced(QR_KERNEL_SMALLN, flops, bytes, s, [&] {
-    return qr::launch_geqrf_midn(A, sAb, sAr, sAc, H, tau, batch, n, s);
+    return qr::launch_geqrf_midn(A, sAb, sAr, sAc, H, sHb, ldh, tau, sTaub, batch, n, s);
   });
 }
 
@@ -353,7 +365,8 @@ int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, f
   if (st != QR_OK || batch == 0 || n == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (n <= kSmallN) return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s));
-  if (n <= qr::midn_max_n()) return to_status(run_midn(A, sAb, sAr, sAc, H, tau, batch, n, s));
+  if (n <= qr::midn_max_n())
+    return to_status(run_midn(A, sAb, sAr, sAc, H, (int64_t)n * n, n, tau, n, batch, n, s));
   return QR_EUNSUPPORTED;
 }
 
@@ -385,7 +398,8 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
 
   const size_t need = qr_geqrf_f32_workspace(batch, n);
   if (workspace_bytes < need || !workspace) return QR_EWORKSPACE;
-  if (midn_route(batch, n, o)) return to_status(run_midn(A, sAb, sAr, sAc, H, tau, batch, n, s));
+  if (midn_route(batch, n, o))
+    return to_status(run_midn(A, sAb, sAr, sAc, H, nn, n, tau, n, batch, n, s));
   // Two T slots per matrix: outer block k uses slot k & 1, so the panels of
   // block k+1 never overwrite T factors that block k's trailing update reads.
   float* Tslot[2] = {static_cast<float*>(workspace),
@@ -427,6 +441,18 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
     float* Tws = Tslot[blk & 1];
     const float* Ab = (direct && J0 == 0) ? A : nullptr;  // source of this block's columns
     const int r = n - J0;
+    // The last r <= 192 columns in one launch of the fused mid-n kernel, in
+    // place on H's trailing r x r block.
+    if (J0 > 0 && midn_route(batch, r, o, true)) {
+      if (rest_pending) {
+        if (hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;
+        rest_pending = false;
+      }
+      float* Hs = H + (int64_t)J0 * n + J0;
+      e = run_midn(Hs, nn, n, 1, Hs, nn, n, tau + J0, n, batch, r, s);
+      if (e != hipSuccess) return QR_ELAUNCH;
+      break;
+    }
     const int nblk = (r + kPanel - 1) / kPanel < P ? (r + kPanel - 1) / kPanel : P;
     // A full 64-column block with enough rows: CholeskyQR2 + reconstruction,
     // then the panels for the matrices it flagged (the rest return at once).

@@ -222,7 +222,8 @@ __device__ __noinline__ void midn_panel_safe(float* pan, float (*zb)[16], float 
 // since phase P's update) and, for a later panel, V and T into LDS.
 template <int NR, int P>
 __device__ __forceinline__ void midn_panel(float (&cs)[4 * NR], MidnShared<NR>& sh, float* Hb,
-                                           float* taub, int n, int k, int g, int lane) {
+                                           int64_t ldh, float* taub, int n, int k, int g,
+                                           int lane) {
   constexpr int NT = NR - P;
   const int kw = min(16, n - 16 * P);  // >= 1: NR = ceil(n / 16)
   const uint64_t kin_mask = __builtin_amdgcn_ballot_w64(k < kw);
@@ -282,7 +283,7 @@ __device__ __forceinline__ void midn_panel(float (&cs)[4 * NR], MidnShared<NR>& 
     for (int t = 0; t < NR; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        if (16 * t + 4 * g + v < n) Hb[(int64_t)(16 * t + v) * n + 16 * P] = cs[4 * t + v];
+        if (16 * t + 4 * g + v < n) Hb[(16 * t + v) * ldh + 16 * P] = cs[4 * t + v];
   }
   if constexpr (P + 1 < NR) {
     // V, unit lower-trapezoidal from the diagonal tile: zero above row kd, one on it.
@@ -302,11 +303,14 @@ __device__ __forceinline__ void midn_panel(float (&cs)[4 * NR], MidnShared<NR>& 
   }
 }
 
+// A and H may be the same memory (the blocked route's last columns, factored
+// in place): every element of a matrix is loaded before the first barrier,
+// and nothing is stored before it.
 template <int NR>
-__global__ __launch_bounds__(64 * NR) void k_geqrf_midn(const float* __restrict__ A, int64_t sAb,
-                                                       int64_t sAr, int64_t sAc,
-                                                       float* __restrict__ H,
-                                                       float* __restrict__ tau, int n) {
+__global__ __launch_bounds__(64 * NR) void k_geqrf_midn(const float* A, int64_t sAb, int64_t sAr,
+                                                       int64_t sAc, float* H, int64_t sHb,
+                                                       int64_t ldh, float* __restrict__ tau,
+                                                       int64_t sTaub, int n) {
   __shared__ __align__(16) MidnShared<NR> sh;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int b = blockIdx.x;
@@ -338,8 +342,8 @@ __global__ __launch_bounds__(64 * NR) void k_geqrf_midn(const float* __restrict_
         cs[4 * t + v] = (row < n && col < n) ? cs[4 * t + v] : 0.0f;
       }
   }
-  float* Hb = H + (int64_t)b * n * n + (int64_t)(4 * g) * n + k;
-  float* taub = tau + (int64_t)b * n;
+  float* Hb = H + (int64_t)b * sHb + (int64_t)(4 * g) * ldh + k;
+  float* taub = tau + (int64_t)b * sTaub;
 
   if (lane == 0) sh.simd[w] = simd_id();
   __syncthreads();
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(64 * NR) void k_geqrf_midn(const float* __restrict_
       __syncthreads();
     }
     if (w == P) {
-      midn_panel<NR, P>(cs, sh, Hb, taub, n, k, g, lane);
+      midn_panel<NR, P>(cs, sh, Hb, ldh, taub, n, k, g, lane);
     } else if constexpr (P > 0) {
       if (w > P) {
         if constexpr (P > 1) {
@@ -383,16 +387,18 @@ __global__ __launch_bounds__(64 * NR) void k_geqrf_midn(const float* __restrict_
 
 int midn_max_n() { return 16 * kMnMaxStrips; }
 
-// H is (batch, n, n) contiguous and tau (batch, n) contiguous; 64 < n <= 192.
+// 64 < n <= 192. H: element (i, j) of matrix b at H[b sHb + i ldh + j]; tau:
+// tau[b sTaub + j]. A and H may be the same memory.
 hipError_t launch_geqrf_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
-                             float* tau, int batch, int n, hipStream_t stream) {
+                             int64_t sHb, int64_t ldh, float* tau, int64_t sTaub, int batch,
+                             int n, hipStream_t stream) {
   const int nr = (n + 15) / 16;
   if (nr < kMnMinStrips || nr > kMnMaxStrips || batch < 1) return hipErrorInvalidValue;
   const dim3 grid(batch), block(64 * nr);
 #define QR_MIDN_CASE(NRV)                                                                  \
   case NRV:                                                                                \
-    hipLaunchKernelGGL((k_geqrf_midn<NRV>), grid, block, 0, stream, A, sAb, sAr, sAc, H, tau, \
-                       n);                                                                 \
+    hipLaunchKernelGGL((k_geqrf_midn<NRV>), grid, block, 0, stream, A, sAb, sAr, sAc, H, sHb, \
+                       ldh, tau, sTaub, n);                                                \
     break;
   switch (nr) {
     QR_MIDN_CASE(5)

@@ -98,8 +98,10 @@ typedef struct qr_options {
   int outer_panels;    /* 16-wide panels per outer block, 1..8; 0 (default): 4. The
                           CholeskyQR2 route needs 4. */
   int midn;            /* 64 < n <= 192: 1 (default) the one-launch fused kernel when
-                          batch * ceil(n / 16) <= 8192, else the blocked route; 0: always
-                          the blocked route; 2: always the fused kernel */
+                          batch * ceil(n / 16) <= 8192, else the blocked route, whose last
+                          r <= 192 columns the kernel factors in place when batch *
+                          ceil(r / 16) <= 2048; 0: the blocked route throughout; 2: the
+                          fused kernel for every such matrix and last block */
 } qr_options;
 
 /* Fills *opts with the defaults qr_geqrf_f32 runs with. */

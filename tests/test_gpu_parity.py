@@ -130,21 +130,49 @@ def test_fused_midn_strided_input(oracle):
 
 @pytest.mark.parametrize("n,batch,fused", [(80, 3, True), (176, 40, True), (192, 682, True),
                                            (192, 683, False), (176, 800, False)])
-def test_geqrf_mid_n_route_choice_bitwise(n, batch, fused):
-    """geqrf's default for 64 < n <= 192: the fused kernel up to batch *
-    ceil(n / 16) = 8192, the blocked route above; midn=2 / midn=0 force one or
-    the other. Each default result equals its forced route bit for bit."""
+def test_geqrf_mid_n_route_choice(oracle, n, batch, fused):
+    """geqrf's default for 64 < n <= 192: the whole matrix in the fused kernel
+    up to batch * ceil(n / 16) = 8192 (bit for bit what midn=2 gives), the
+    blocked route above. midn=0 is the blocked route throughout."""
     _say(f"mid-n route choice n={n} batch={batch} fused={fused}")
     A = _gauss(batch, n, seed=n + batch).to(DEV)
     H, tau = hip_qr.geqrf(A)
     Hf, tf = hip_qr.geqrf(A, options=hip_qr.options(midn=2))
     Hb, tb = hip_qr.geqrf(A, options=hip_qr.options(midn=0))
     torch.cuda.synchronize()
-    Hx, tx = (Hf, tf) if fused else (Hb, tb)
-    assert torch.equal(H, Hx) and torch.equal(tau, tx)
+    assert (torch.equal(H, Hf) and torch.equal(tau, tf)) == fused
     assert not torch.equal(Hf, Hb)  # two different kernels: not the same bits
     res = checker.check(A.cpu(), H.cpu(), tau.cpu())
     assert res.passed, res.as_dict()
+    idx = [0, batch - 1]
+    A_s = A[idx].cpu().numpy()
+    H_ref, tau_ref = oracle.geqrf(A_s, nb=16)
+    assert_parity(A_s, H[idx].cpu().numpy(), tau[idx].cpu().numpy(), H_ref, tau_ref,
+                  what=f"route choice n={n} b={batch}")
+
+
+@pytest.mark.parametrize("n,batch,tail", [(352, 3, True), (300, 40, True), (1100, 2, True),
+                                          (300, 500, False)])
+def test_geqrf_last_columns_in_fused_kernel(oracle, n, batch, tail):
+    """The blocked route hands its last r <= 192 columns to the fused kernel,
+    in place, while batch * ceil(r / 16) <= 2048 (midn=2 always, midn=0
+    never): the default equals midn=2 bit for bit when the bound holds and
+    midn=0 when it does not, and matches the oracle."""
+    _say(f"last columns in the fused kernel n={n} batch={batch} tail={tail}")
+    A = _gauss(batch, n, seed=n + 2 * batch).to(DEV)
+    H, tau = hip_qr.geqrf(A)
+    Hf, tf = hip_qr.geqrf(A, options=hip_qr.options(midn=2))
+    Hb, tb = hip_qr.geqrf(A, options=hip_qr.options(midn=0))
+    torch.cuda.synchronize()
+    Hx, tx = (Hf, tf) if tail else (Hb, tb)
+    assert torch.equal(H, Hx) and torch.equal(tau, tx)
+    assert not torch.equal(Hf, Hb)
+    idx = [0, batch - 1]
+    A_s = A[idx].cpu().numpy()
+    H_ref, tau_ref = oracle.geqrf(A_s, nb=16)
+    for Hy, ty, what in ((Hf, tf, "fused tail"), (Hb, tb, "blocked tail")):
+        assert_parity(A_s, Hy[idx].cpu().numpy(), ty[idx].cpu().numpy(), H_ref, tau_ref,
+                      what=f"n={n} b={batch} {what}")
 
 
 def test_fused_midn_padded_input_bitwise(oracle):
