@@ -21,7 +21,8 @@
 
 namespace qr {
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
-                               float* tau, int batch, int n, hipStream_t stream);
+                               int64_t sHb, int64_t ldh, float* tau, int64_t sTaub, int batch,
+                               int n, hipStream_t stream);
 hipError_t launch_geqrf_midn(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
                              int64_t sHb, int64_t ldh, float* tau, int64_t sTaub, int batch,
                              int n, hipStream_t stream);
@@ -215,12 +216,14 @@ int check_geqrf_args(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, cons
   return QR_OK;
 }
 
-hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H, float* tau,
-                      int batch, int n, hipStream_t s) {
+// H and tau at strides (sHb, ldh, 1) and (sTaub, 1); A may be H itself.
+hipError_t run_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
+                      int64_t sHb, int64_t ldh, float* tau, int64_t sTaub, int batch, int n,
+                      hipStream_t s) {
   const double flops = 4.0 / 3.0 * n * n * (double)n * batch;
   const double bytes = (2.0 * n * n + n) * 4.0 * batch;
   return traced(QR_KERNEL_SMALLN, flops, bytes, s, [&] {
-    return qr::launch_geqrf_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s);
+    return qr::launch_geqrf_smalln(A, sAb, sAr, sAc, H, sHb, ldh, tau, sTaub, batch, n, s);
   });
 }
 
@@ -364,7 +367,8 @@ int qr_fused_smalln_f32(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, f
   int st = check_geqrf_args(A, sAb, sAr, sAc, H, tau, batch, n);
   if (st != QR_OK || batch == 0 || n == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (n <= kSmallN) return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s));
+  if (n <= kSmallN)
+    return to_status(run_smalln(A, sAb, sAr, sAc, H, (int64_t)n * n, n, tau, n, batch, n, s));
   if (n <= qr::midn_max_n())
     return to_status(run_midn(A, sAb, sAr, sAc, H, (int64_t)n * n, n, tau, n, batch, n, s));
   return QR_EUNSUPPORTED;
@@ -394,7 +398,8 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
   if (st != QR_OK || batch == 0 || n == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nn = (int64_t)n * n;
-  if (n <= kSmallN) return to_status(run_smalln(A, sAb, sAr, sAc, H, tau, batch, n, s));
+  if (n <= kSmallN)
+    return to_status(run_smalln(A, sAb, sAr, sAc, H, (int64_t)n * n, n, tau, n, batch, n, s));
 
   const size_t need = qr_geqrf_f32_workspace(batch, n);
   if (workspace_bytes < need || !workspace) return QR_EWORKSPACE;
@@ -443,6 +448,17 @@ int qr_geqrf_f32_ex(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float
     const int r = n - J0;
     // The last r <= 192 columns in one launch of the fused mid-n kernel, in
     // place on H's trailing r x r block.
+    // The last <= 64 columns: one small-n launch, in place (not with midn = 0).
+    if (J0 > 0 && r <= kSmallN && o.midn != 0) {
+      if (rest_pending) {
+        if (hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;
+        rest_pending = false;
+      }
+      float* Hs = H + (int64_t)J0 * n + J0;
+      e = run_smalln(Hs, nn, n, 1, Hs, nn, n, tau + J0, n, batch, r, s);
+      if (e != hipSuccess) return QR_ELAUNCH;
+      break;
+    }
     if (J0 > 0 && midn_route(batch, r, o, true)) {
       if (rest_pending) {
         if (hipStreamWaitEvent(s, la.rest_done, 0) != hipSuccess) return QR_ELAUNCH;

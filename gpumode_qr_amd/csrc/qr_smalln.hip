@@ -42,13 +42,16 @@ struct SmallnShared {
   float save[(S * 4 * 64) > 16 * (16 * S + 4) ? (S * 4 * 64) : 16 * (16 * S + 4)];
 };
 
-template <int S, bool kVec>
+// kStrided: H and tau at the strides given (the blocked route's last columns,
+// in place); otherwise H is (batch, n, n) and tau (batch, n), contiguous, and
+// the strides are not read.
+template <int S, bool kVec, bool kStrided>
 // At least two waves per SIMD (<= 256 VGPRs): 2048 matrices fill every SIMD
 // twice, and the second wave hides the first one's per-column latency.
 __global__ __launch_bounds__(64 * kSnWaves, 2)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
     const float* __restrict__ A, int64_t sAb, int64_t sAr, int64_t sAc, float* __restrict__ H,
-    float* __restrict__ tau, int batch, int n) {
+    int64_t sHb, int64_t ldh, float* __restrict__ tau, int64_t sTaub, int batch, int n) {
   __shared__ __align__(16) SmallnShared<S> shm[kSnWaves];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int b = blockIdx.x * kSnWaves + w;
@@ -125,14 +128,19 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
 
   // Strip s of H, stored as soon as its panel is packed (no later step
   // touches it), so the stores of strips 0 .. S-2 overlap the later panels.
-  float* Hb = H + (int64_t)b * n * n + (int64_t)(4 * g) * n + k;
+  if constexpr (!kStrided) {
+    sHb = (int64_t)n * n;
+    ldh = n;
+    sTaub = n;
+  }
+  float* Hb = H + (int64_t)b * sHb + (int64_t)(4 * g) * ldh + k;
   auto store_strip = [&](auto SI) {
     constexpr int s = decltype(SI)::value;
     if (n == 16 * S) {
 #pragma unroll
       for (int t = 0; t < S; ++t)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
+        for (int v = 0; v < 4; ++v) Hb[(16 * t + v) * ldh + 16 * s] = c[s][4 * t + v];
     } else {
       int kk = k0, gg = g0;
       asm volatile("" : "+v"(kk), "+v"(gg));
@@ -141,7 +149,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (16 * t + 4 * gg + v < n && 16 * s + kk < n)
-            Hb[(int64_t)(16 * t + v) * n + 16 * s] = c[s][4 * t + v];
+            Hb[(16 * t + v) * ldh + 16 * s] = c[s][4 * t + v];
     }
   };
 
@@ -190,7 +198,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
     const float my_beta = kin ? -rf.x : 0.0f, my_tau = kin ? rf.y : 0.0f;
     const float my_gamma = col.gamma, my_pre = col.pre;
 
-    if (g == 0 && kin) tau[(int64_t)b * n + 16 * p + k] = my_tau;
+    if (g == 0 && kin) tau[(int64_t)b * sTaub + 16 * p + k] = my_tau;
 
     // Final packing of the panel: R above the diagonal, beta on it, the
     // essential reflector v = (x pre) gamma below it.
@@ -285,23 +293,36 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
 
 }
 
-// Host-side dispatch over the number of 16-column strips. H is (batch, n, n)
-// contiguous and tau (batch, n) contiguous.
+// Host-side dispatch over the number of 16-column strips. H: element (i, j) of
+// matrix b at H[b sHb + i ldh + j]; tau: tau[b sTaub + j]. A may be H itself
+// (the blocked route's last columns, factored in place): every value a wave
+// stores is computed from what it loaded from that same address, so no store
+// can overtake the load it overwrites (the restrict qualifiers allow no
+// reordering that matters here).
 hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t sAc, float* H,
-                               float* tau, int batch, int n, hipStream_t stream) {
+                               int64_t sHb, int64_t ldh, float* tau, int64_t sTaub, int batch,
+                               int n, hipStream_t stream) {
   if (n < 1 || n > 64 || batch < 1) return hipErrorInvalidValue;
   const dim3 grid((batch + kSnWaves - 1) / kSnWaves), block(64 * kSnWaves);
   const bool vec = n == 64 && sAc == 1 && (sAr % 4) == 0 && (sAb % 4) == 0 &&
                    (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  const bool strided = !(sHb == (int64_t)n * n && ldh == n && sTaub == n);
+#define QR_SMALLN_LAUNCH(SV, VEC, STR)                                                       \
+  hipLaunchKernelGGL((k_geqrf_smalln<SV, VEC, STR>), grid, block, 0, stream, A, sAb, sAr, sAc, \
+                     H, sHb, ldh, tau, sTaub, batch, n)
   if (vec) {
-    hipLaunchKernelGGL((k_geqrf_smalln<4, true>), grid, block, 0, stream, A, sAb, sAr, sAc, H,
-                       tau, batch, n);
+    if (strided)
+      QR_SMALLN_LAUNCH(4, true, true);
+    else
+      QR_SMALLN_LAUNCH(4, true, false);
     return hipGetLastError();
   }
-#define QR_SMALLN_CASE(SV)                                                                  \
-  case SV:                                                                                  \
-    hipLaunchKernelGGL((k_geqrf_smalln<SV, false>), grid, block, 0, stream, A, sAb, sAr, sAc, \
-                       H, tau, batch, n);                                                   \
+#define QR_SMALLN_CASE(SV)               \
+  case SV:                               \
+    if (strided)                         \
+      QR_SMALLN_LAUNCH(SV, false, true); \
+    else                                 \
+      QR_SMALLN_LAUNCH(SV, false, false); \
     break;
   switch ((n + 15) / 16) {
     QR_SMALLN_CASE(1)
@@ -312,6 +333,7 @@ hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t
       return hipErrorInvalidValue;
   }
 #undef QR_SMALLN_CASE
+#undef QR_SMALLN_LAUNCH
   return hipGetLastError();
 }
 

@@ -100,8 +100,9 @@ typedef struct qr_options {
   int midn;            /* 64 < n <= 192: 1 (default) the one-launch fused kernel when
                           batch * ceil(n / 16) <= 8192, else the blocked route, whose last
                           r <= 192 columns the kernel factors in place when batch *
-                          ceil(r / 16) <= 2048; 0: the blocked route throughout; 2: the
-                          fused kernel for every such matrix and last block */
+                          ceil(r / 16) <= 2048, and whose last r <= 64 columns the small-n
+                          kernel factors in place; 0: the blocked route throughout; 2: the
+                          fused kernels for every such matrix and last block */
 } qr_options;
 
 /* Fills *opts with the defaults qr_geqrf_f32 runs with. */

@@ -154,23 +154,23 @@ def test_geqrf_mid_n_route_choice(oracle, n, batch, fused):
 @pytest.mark.parametrize("n,batch,tail", [(352, 3, True), (300, 40, True), (1100, 2, True),
                                           (300, 500, False)])
 def test_geqrf_last_columns_in_fused_kernel(oracle, n, batch, tail):
-    """The blocked route hands its last r <= 192 columns to the fused kernel,
-    in place, while batch * ceil(r / 16) <= 2048 (midn=2 always, midn=0
-    never): the default equals midn=2 bit for bit when the bound holds and
-    midn=0 when it does not, and matches the oracle."""
+    """The blocked route hands its last r <= 192 columns to the fused mid-n
+    kernel, in place, while batch * ceil(r / 16) <= 2048 (midn=2 always,
+    midn=0 never), and otherwise its last r <= 64 columns to the small-n
+    kernel: the default equals midn=2 bit for bit when the bound holds and
+    neither forced route when it does not. All three match the oracle."""
     _say(f"last columns in the fused kernel n={n} batch={batch} tail={tail}")
     A = _gauss(batch, n, seed=n + 2 * batch).to(DEV)
     H, tau = hip_qr.geqrf(A)
     Hf, tf = hip_qr.geqrf(A, options=hip_qr.options(midn=2))
     Hb, tb = hip_qr.geqrf(A, options=hip_qr.options(midn=0))
     torch.cuda.synchronize()
-    Hx, tx = (Hf, tf) if tail else (Hb, tb)
-    assert torch.equal(H, Hx) and torch.equal(tau, tx)
-    assert not torch.equal(Hf, Hb)
+    assert (torch.equal(H, Hf) and torch.equal(tau, tf)) == tail
+    assert not torch.equal(H, Hb) and not torch.equal(Hf, Hb)
     idx = [0, batch - 1]
     A_s = A[idx].cpu().numpy()
     H_ref, tau_ref = oracle.geqrf(A_s, nb=16)
-    for Hy, ty, what in ((Hf, tf, "fused tail"), (Hb, tb, "blocked tail")):
+    for Hy, ty, what in ((H, tau, "default"), (Hf, tf, "fused tail"), (Hb, tb, "blocked")):
         assert_parity(A_s, Hy[idx].cpu().numpy(), ty[idx].cpu().numpy(), H_ref, tau_ref,
                       what=f"n={n} b={batch} {what}")
 
