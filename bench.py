@@ -59,13 +59,15 @@ CHAMPION_PROXY_MS = {2: 0.1018, 3: 6.966, 4: 8.245, 5: 20.20}
 # profile_run runs first (FETCH x2.000, WRITE x1.000). Counters cannot be read
 # from inside this process; rerun those commands after changing a kernel.
 HBM_MIB_PER_CALL = {
-    "smalln": {2: 32.7 + 46.8},
+    # k_geqrf_smalln (cfg 2; the last 64 columns at cfg 3) and k_geqrf_midn (the
+    # last 192 columns at cfgs 4-5), both traced as "smalln".
+    "smalln": {2: 32.7 + 47.0, 3: 10.7 + 10.2, 4: 13.6 + 9.0, 5: 6.8 + 2.3},
     # k_panel + k_panel_seq (fallback panels of the CholeskyQR2 route), both
     # traced as "panel".
-    "panel": {3: 1146.7 + 298.6, 4: 4.9 + 1.3, 5: 7.4 + 3.9},
-    "trail": {3: 2489.2 + 1697.5, 4: 1803.8 + 1433.8, 5: 3254.8 + 2807.0},
+    "panel": {3: 1585.3 + 368.6, 4: 0.5 + 0.0, 5: 5.1 + 2.8},
+    "trail": {3: 2494.9 + 1698.1, 4: 1795.4 + 1429.8, 5: 3251.2 + 2809.7},
     # k_cq_gram + k_cq_chol1 + k_cq_recon + k_cq_form of the CholeskyQR2 route.
-    "cholqr": {3: 194.8 + 118.9, 4: 379.5 + 213.5, 5: 383.1 + 196.6},
+    "cholqr": {4: 359.8 + 200.1, 5: 377.0 + 193.2},
 }
 RIDGE_FLOP_PER_BYTE = FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
