@@ -23,7 +23,7 @@ ARCH = "gfx950"
 
 SOURCES = [
     "qr_smalln.hip", "qr_midn.hip", "qr_blocked.hip", "qr_cholqr.hip", "qr_apply.hip", "qr_larft.hip",
-    "qr_copy.hip", "qr_api.hip",
+    "qr_copy.hip", "qr_orgqr_smalln.hip", "qr_api.hip",
 ]
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (the host

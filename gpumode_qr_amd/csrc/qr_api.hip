@@ -59,6 +59,9 @@ hipError_t launch_apply(const float* V, int64_t sVb, int64_t ldv, float* C, int6
                         int64_t ldc, int nblk, int r, int ncols, const float* Tws, int64_t sTwb,
                         bool trans, int kv_last, int batch, hipStream_t stream);
 hipError_t launch_eye(float* Q, int64_t sQb, int64_t ldq, int batch, int n, hipStream_t stream);
+hipError_t launch_orgqr_smalln(const float* H, int64_t sHb, int64_t ldh, const float* tau,
+                               int64_t sTaub, float* Q, int64_t sQb, int64_t ldq, int batch,
+                               int n, hipStream_t stream);
 }  // namespace qr
 
 namespace {
@@ -731,6 +734,12 @@ int qr_orgqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int
     return QR_EINVAL;
   if (!workspace || workspace_bytes < qr_ormqr_f32_workspace(batch, n)) return QR_EWORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n <= kSmallN) {  // one wavefront per matrix forms Q in registers: one launch
+    const double flops = 4.0 / 3.0 * n * n * (double)n * batch;
+    return to_status(traced(QR_KERNEL_APPLY, flops, (2.0 * n * n + n) * 4.0 * batch, s, [&] {
+      return qr::launch_orgqr_smalln(H, sHb, ldh, tau, sTaub, Q, sQb, ldq, batch, n, s);
+    }));
+  }
   const hipError_t e = traced(QR_KERNEL_COPY, 0.0, (double)n * n * 4.0 * batch, s,
                               [&] { return qr::launch_eye(Q, sQb, ldq, batch, n, s); });
   if (e != hipSuccess) return to_status(e);

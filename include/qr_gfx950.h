@@ -213,7 +213,9 @@ int qr_ormqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int
  * Form Q (n x n, row stride ldq; must not overlap H) of a factorisation
  * (H, tau): Q := Q I (LAPACK sorgqr). Replaces
  * torch.linalg.householder_product(H, tau) as used by the reference's gates
- * (src/qrbench/checker.py:129).
+ * (src/qrbench/checker.py:129). n <= 64 runs one launch (a wavefront per
+ * matrix, Q formed in registers); larger n the per-panel T rebuild and the
+ * block-reflector application.
  */
 int qr_orgqr_f32(const float* H, int64_t sHb, int64_t ldh, const float* tau, int64_t sTaub,
                  float* Q, int64_t sQb, int64_t ldq, int n, int batch, void* workspace,
