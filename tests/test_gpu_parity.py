@@ -175,6 +175,25 @@ def test_geqrf_last_columns_in_fused_kernel(oracle, n, batch, tail):
                       what=f"n={n} b={batch} {what}")
 
 
+@pytest.mark.parametrize("n,batch", [(80, 1500), (192, 600)])
+def test_fused_midn_many_matrices(oracle, n, batch):
+    """Many workgroups per CU over the launch (the fused kernel's largest
+    default batches): gates on the whole batch, oracle parity on three
+    matrices spread over it."""
+    _say(f"fused mid-n many matrices n={n} batch={batch}")
+    A = _gauss(batch, n, seed=n + 3 * batch)
+    H, tau = hip_qr.fused_smalln(A.to(DEV))
+    torch.cuda.synchronize()
+    H, tau = H.cpu(), tau.cpu()
+    assert torch.isfinite(H).all() and torch.isfinite(tau).all()
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+    idx = [0, batch // 2, batch - 1]
+    H_ref, tau_ref = oracle.geqrf(A[idx].numpy())
+    assert_parity(A[idx].numpy(), H[idx].numpy(), tau[idx].numpy(), H_ref, tau_ref,
+                  what=f"midn many n={n} b={batch}")
+
+
 def test_fused_midn_padded_input_bitwise(oracle):
     """Unit column stride with padded rows and batch is read in place; the
     column-major view of the same values gives the same bits."""
