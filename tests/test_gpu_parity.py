@@ -379,6 +379,21 @@ def test_geqrf_blocked_vs_oracle(oracle, n):
     assert res.passed, res.as_dict()
 
 
+@pytest.mark.parametrize("n", [65, 97, 129, 150, 200, 257, 270, 333])
+def test_geqrf_default_route_vs_oracle(oracle, n):
+    """The default route at sizes whose last columns are a ragged fused tail:
+    the whole matrix in the mid-n kernel (n <= 192), or outer blocks and then
+    the last n - 64 k <= 192 columns in place (r = 136, 129, 142, 141: last
+    strips of 8, 1, 14 and 13 columns)."""
+    _say(f"geqrf default route n={n}")
+    A = _gauss(2, n, seed=n + 29)
+    H, tau = _run(A)
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"default n={n}")
+    res = checker.check(A, H, tau)
+    assert res.passed, res.as_dict()
+
+
 def test_geqrf_matches_mkl_golden_fixtures():
     from tests.test_oracle import _golden
 
