@@ -36,10 +36,9 @@ constexpr int kVStride = 20;
 // 16-row tiles of V staged per wave at a time (LDS budget: NW * tiles * 1.25 KB).
 // Two at 8 waves: the 512-row panel kernel then needs 38 KB of LDS, so three of
 // its workgroups share a CU. The 16-wave kernels stage four, except for strips
-// of 2049-4096 rows (RL = 64): with two (58 KB instead of 99 KB) the route's
-// Gram workgroups (80 KB) fit beside a trailing-update workgroup, which at
-// b2 n4096 gains more (7.30 -> 7.18 ms) than the shallower staging costs; at
-// 2048 rows and below it costs more (b64 n1024 2.29 -> 2.37 ms).
+// of 2049-4096 rows (RL = 64), which stage two: measured b2 n4096 7.30 -> 7.15
+// ms (58 KB of LDS instead of 99 KB, 16 bytes of spills per lane instead of
+// 36); at 2048 rows and below two cost more (b64 n1024 2.29 -> 2.37 ms).
 #ifndef QR_STAGE_TILES_MAX
 #define QR_STAGE_TILES_MAX 2
 #endif
