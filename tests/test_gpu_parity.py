@@ -542,6 +542,29 @@ def test_blocked_extreme_columns_vs_oracle(oracle, n, cols, scale):
     assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref, what=f"n={n} x{scale:g}")
 
 
+@pytest.mark.parametrize("scale", [1e-30, 1e25, 1e-40], ids=["tiny", "huge", "denormal"])
+def test_default_route_extreme_columns_vs_oracle(oracle, scale):
+    """The default route at n = 300, batch 2: CholeskyQR2 on the 300- and
+    236-row outer blocks (column 20 fails its guard and goes back to the
+    panels), then the last 172 columns in the fused mid-n kernel in place,
+    where columns 150, 200 (zero) and 290 take its rare path: the panel is
+    refactored from its saved copy with slarfg's scaled branches."""
+    _say(f"default route extreme columns n=300 scale={scale:g}")
+    A = _gauss(2, 300, seed=301)
+    A[0, :, 20] *= scale
+    A[0, :, 200] = 0.0
+    A[1, :, 150] *= scale
+    A[1, :, 290] *= scale
+    H, tau = _run(A)
+    Hf, tf = _run(A, midn=2)
+    assert torch.equal(H, Hf) and torch.equal(tau, tf)  # the tail is the fused kernel's
+    assert torch.isfinite(H).all() and torch.isfinite(tau).all()
+    assert tau[0, 200] == 0
+    H_ref, tau_ref = oracle.geqrf(A.numpy(), nb=16)
+    assert_parity(A.numpy(), H.numpy(), tau.numpy(), H_ref, tau_ref,
+                  what=f"default n=300 x{scale:g}")
+
+
 def test_side_stream_and_strided_input_bitwise():
     """The call runs on the caller's current stream (a non-default one here), and
     a transposed (column-major) input takes the same kernels after the strided
