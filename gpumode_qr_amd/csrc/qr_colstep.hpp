@@ -232,9 +232,11 @@ __device__ __forceinline__ void smalln_step(float (&cp)[4 * S], Sh& sh, float* z
   float ds, e, dpart;
   rows16_sum_bcast<gj>(dsum, cp[4 * P + vj], ds, e, dpart);
   const float sigma = readlane_f(dpart, JJ);  // lane JJ's dot is x^T x
-  // No rows below the diagonal (the last column): tau = 0. With n = 16 S
-  // known (kFullN) that is a compile-time fact, which saves the selects of
-  // a runtime test in every step (cfg 2: 44.8 -> 43.0 us).
+  // No rows below the diagonal (the last column): tau = 0. When the caller
+  // knows the panel is full (kFullN: n = 16 S, or any panel before the last,
+  // whose columns all lie before column n - 1 since S = ceil(n / 16)), that
+  // is a compile-time fact, which saves the selects of a runtime test in
+  // every step (cfg 2: 44.8 -> 43.0 us).
   const bool identity = kFullN ? (16 * P + JJ == 16 * S - 1) : (j >= n - 1);
 
   Reflector R;

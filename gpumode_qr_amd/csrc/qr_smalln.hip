@@ -156,9 +156,12 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
   static_for<0, S>([&](auto PI) {
     constexpr int p = decltype(PI)::value;
     constexpr int NT = S - p;  // row tiles at or below the panel's diagonal tile
-    const int kw = kVec ? 16 : min(16, n - 16 * p);  // >= 1: S = ceil(n / 16)
+    // S = ceil(n / 16): every panel but the last has all 16 columns and none of
+    // them is column n - 1, so only the last panel of a ragged n tests them.
+    constexpr bool kFull = kVec || p + 1 < S;
+    const int kw = kFull ? 16 : min(16, n - 16 * p);  // >= 1
     // Lanes whose column exists (wave-uniform mask).
-    const uint64_t kin_mask = kVec ? ~uint64_t(0) : __builtin_amdgcn_ballot_w64(k0 < kw);
+    const uint64_t kin_mask = kFull ? ~uint64_t(0) : __builtin_amdgcn_ballot_w64(k0 < kw);
 
     // The steps only modify the panel's own rows >= 16 p: keep a copy for the
     // safe re-run (conflict-free b128 stores, lane-consecutive).
@@ -171,7 +174,8 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
     int bad = 0;
     static_for<0, 16>([&](auto JI) {
       constexpr int jj = decltype(JI)::value;
-      if (jj < kw) smalln_step<S, p, jj, false, kVec>(c[p], sh, zrow, n, kin_mask, bad, col);
+      if (kFull || jj < kw)
+        smalln_step<S, p, jj, false, kFull>(c[p], sh, zrow, n, kin_mask, bad, col);
     });
     if (__builtin_amdgcn_readfirstlane(bad)) [[unlikely]] {
       wave_lds_sync();
