@@ -2,7 +2,9 @@
 
 Usage: ``python -m gpumode_qr_amd.csrc.build`` (also called by
 ``__graft_entry__.build()``). Each ``.hip`` file is compiled to an object in
-parallel, then linked into ``gpumode_qr_amd/libqr_gfx950.so``.
+parallel, then linked into ``gpumode_qr_amd/libqr_gfx950.so``. The default
+build also compiles ``qr_fastcall.c`` (the CPython binding of ``qr_geqrf_f32``)
+with the host C compiler into ``gpumode_qr_amd/_qr_fastcall*.so``.
 """
 
 from __future__ import annotations
@@ -11,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -19,6 +22,7 @@ PKG = CSRC.parent
 REPO = PKG.parent
 OUT_DIR = PKG / "_build"
 LIB = PKG / "libqr_gfx950.so"
+FASTCALL = PKG / ("_qr_fastcall" + sysconfig.get_config_var("EXT_SUFFIX"))
 ARCH = "gfx950"
 
 SOURCES = [
@@ -74,7 +78,26 @@ def build(verbose: bool = False, out: Path = LIB, defines: tuple[str, ...] = ())
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")
+    if out == LIB:
+        build_fastcall(verbose)
     return out
+
+
+def build_fastcall(verbose: bool = False) -> Path:
+    """The CPython binding of ``qr_geqrf_f32`` (``qr_fastcall.c``): Python's
+    headers only, no HIP."""
+    cc = os.environ.get("CC") or shutil.which("gcc") or "cc"
+    tmp = FASTCALL.with_name(FASTCALL.name + ".tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror",
+           f"-I{sysconfig.get_paths()['include']}", str(CSRC / "qr_fastcall.c"), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("C compiler failed on qr_fastcall.c")
+    os.replace(tmp, FASTCALL)
+    if verbose:
+        print(f"built {FASTCALL}")
+    return FASTCALL
 
 
 if __name__ == "__main__":

@@ -19,6 +19,11 @@ import torch
 
 from . import _lib
 
+try:  # CPython binding of qr_geqrf_f32 (csrc/qr_fastcall.c), built with the library
+    from . import _qr_fastcall
+except ImportError:
+    _qr_fastcall = None
+
 PANEL = 16  # panel width of the blocked route
 SMALL_N = 64  # largest n of the fused one-wave-per-matrix route (no workspace)
 
@@ -43,6 +48,26 @@ def _stream_of(index: int) -> int:
 
 def _current_device() -> int:
     return _cur_device() if _cur_device is not None else torch.cuda.current_device()
+
+
+# qr_geqrf_f32 as geqrf calls it, and the library it was taken from: through
+# the CPython binding when it is built (about 0.1 us per call against about 1 us
+# for ctypes' conversion of eleven arguments; the call sits inside every
+# event-timed call), else through ctypes. Both call the same library function.
+_geqrf_lib = None
+_geqrf_fn = None
+
+
+def _geqrf_entry(lib):
+    global _geqrf_lib, _geqrf_fn
+    if _geqrf_lib is not lib:
+        if _qr_fastcall is not None:
+            _qr_fastcall.bind(ctypes.cast(lib.qr_geqrf_f32, ctypes.c_void_p).value)
+            _geqrf_fn = _qr_fastcall.geqrf
+        else:
+            _geqrf_fn = lib.qr_geqrf_f32
+        _geqrf_lib = lib
+    return _geqrf_fn
 
 
 def _check_input(A: torch.Tensor) -> None:
@@ -100,7 +125,8 @@ def geqrf(A: torch.Tensor, workspace: torch.Tensor | None = None,
     args = (A.data_ptr(), sb, sr, sc, H.data_ptr(), tau.data_ptr(), b, n, ws_ptr, ws_len)
     index = A.get_device()
     if options is None:
-        call = lambda: lib.qr_geqrf_f32(*args, _stream_of(index))  # noqa: E731
+        fn = _geqrf_entry(lib)
+        call = lambda: fn(*args, _stream_of(index))  # noqa: E731
     else:
         call = lambda: lib.qr_geqrf_f32_ex(*args, ctypes.byref(options),  # noqa: E731
                                            _stream_of(index))

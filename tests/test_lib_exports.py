@@ -128,3 +128,32 @@ def test_route_codes_lie_inside_the_workspace(lib):
         assert 0 < off and off + 4 * batch <= lib.qr_geqrf_f32_workspace(batch, n)
         assert off % 4 == 0
     assert lib.qr_geqrf_f32_route_codes_offset(8, 64) == 0  # fused small-n route: none
+
+
+def test_fastcall_binding_matches_ctypes(lib):
+    """geqrf's CPython binding of qr_geqrf_f32 (built with the library) returns
+    the library's own status codes on the validation paths, and rejects
+    arguments that do not fit the C parameters instead of truncating them."""
+    from gpumode_qr_amd import hip_qr
+    from gpumode_qr_amd.csrc import build
+
+    if not build.FASTCALL.exists():
+        build.build_fastcall()
+        pytest.skip("binding built by this test: rerun to load it")
+    fn = hip_qr._geqrf_entry(lib)
+    assert hip_qr._qr_fastcall is not None and fn is hip_qr._qr_fastcall.geqrf
+    cases = [
+        (0, 1, 1, 1, 0, 0, -1, 4, None, 0, 0),       # negative batch
+        (0, 1, 1, 1, 0, 0, 4, -1, None, 0, 0),       # negative n
+        (0, 1, 1, 1, 0, 0, 1, 70000, None, 0, 0),    # n above qr_max_n
+        (0, 1, 1, 1, 0, 0, 1, 4, None, 0, 0),        # null pointers
+        (16, 64 * 64, 64, 1, 16, 16, 3, 64, None, 0, 0),  # H aliases A
+    ]
+    for args in cases:
+        assert fn(*args) == lib.qr_geqrf_f32(*args) != 0, args
+    with pytest.raises(OverflowError):
+        fn(0, 1, 1, 1, 0, 0, 2**31, 4, None, 0, 0)
+    with pytest.raises(OverflowError):
+        fn(0, 1, 1, 1, 0, 0, 1, 4, None, -1, 0)
+    with pytest.raises(TypeError):
+        fn(0, 1, 1, 1, 0, 0, 1, 4, None, 0)
