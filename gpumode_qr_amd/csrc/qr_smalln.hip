@@ -44,8 +44,8 @@ struct SmallnShared {
 
 // kStrided: H and tau at the strides given (the blocked route's last columns,
 // in place); otherwise H is (batch, n, n) and tau (batch, n), contiguous, and
-// the strides are not read.
-template <int S, bool kVec, bool kStrided>
+// the strides are not read. kWhole: n = 16 S (implied by kVec).
+template <int S, bool kVec, bool kStrided, bool kWhole>
 // At least two waves per SIMD (<= 256 VGPRs): 2048 matrices fill every SIMD
 // twice, and the second wave hides the first one's per-column latency.
 __global__ __launch_bounds__(64 * kSnWaves, 2)
@@ -158,7 +158,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void k_geqrf_smalln(
     constexpr int NT = S - p;  // row tiles at or below the panel's diagonal tile
     // S = ceil(n / 16): every panel but the last has all 16 columns and none of
     // them is column n - 1, so only the last panel of a ragged n tests them.
-    constexpr bool kFull = kVec || p + 1 < S;
+    constexpr bool kFull = kVec || kWhole || p + 1 < S;
     const int kw = kFull ? 16 : min(16, n - 16 * p);  // >= 1
     // Lanes whose column exists (wave-uniform mask).
     const uint64_t kin_mask = kFull ? ~uint64_t(0) : __builtin_amdgcn_ballot_w64(k0 < kw);
@@ -311,22 +311,30 @@ hipError_t launch_geqrf_smalln(const float* A, int64_t sAb, int64_t sAr, int64_t
   const bool vec = n == 64 && sAc == 1 && (sAr % 4) == 0 && (sAb % 4) == 0 &&
                    (reinterpret_cast<uintptr_t>(A) & 15) == 0;
   const bool strided = !(sHb == (int64_t)n * n && ldh == n && sTaub == n);
-#define QR_SMALLN_LAUNCH(SV, VEC, STR)                                                       \
-  hipLaunchKernelGGL((k_geqrf_smalln<SV, VEC, STR>), grid, block, 0, stream, A, sAb, sAr, sAc, \
-                     H, sHb, ldh, tau, sTaub, batch, n)
+  const bool whole = n % 16 == 0;
+#define QR_SMALLN_LAUNCH(SV, VEC, STR, WH)                                                  \
+  hipLaunchKernelGGL((k_geqrf_smalln<SV, VEC, STR, WH>), grid, block, 0, stream, A, sAb, sAr, \
+                     sAc, H, sHb, ldh, tau, sTaub, batch, n)
   if (vec) {
     if (strided)
-      QR_SMALLN_LAUNCH(4, true, true);
+      QR_SMALLN_LAUNCH(4, true, true, true);
     else
-      QR_SMALLN_LAUNCH(4, true, false);
+      QR_SMALLN_LAUNCH(4, true, false, true);
     return hipGetLastError();
   }
-#define QR_SMALLN_CASE(SV)               \
-  case SV:                               \
-    if (strided)                         \
-      QR_SMALLN_LAUNCH(SV, false, true); \
-    else                                 \
-      QR_SMALLN_LAUNCH(SV, false, false); \
+#define QR_SMALLN_CASE(SV)                        \
+  case SV:                                        \
+    if (strided) {                                \
+      if (whole)                                  \
+        QR_SMALLN_LAUNCH(SV, false, true, true);  \
+      else                                        \
+        QR_SMALLN_LAUNCH(SV, false, true, false); \
+    } else {                                      \
+      if (whole)                                  \
+        QR_SMALLN_LAUNCH(SV, false, false, true); \
+      else                                        \
+        QR_SMALLN_LAUNCH(SV, false, false, false); \
+    }                                             \
     break;
   switch ((n + 15) / 16) {
     QR_SMALLN_CASE(1)
